@@ -1,0 +1,166 @@
+/* kern_amd — the C ABI of the MI355X-native MXFP4 matmul path.
+ *
+ * Two layers, both plain C (pointers, sizes, a hipStream_t passed as void*):
+ *
+ *  1. Module layer: the thin host->HIP layer that kern's runtime calls in place of its CUDA driver
+ *     calls. It loads a SHA-256-pinned gfx950 code object, resolves entries, checks a launch's
+ *     kernel-argument layout against the code object's own metadata, launches, and captures /
+ *     replays hipGraphs.
+ *  2. Op layer: one entry point per manifest op of the path, same parameter order and meaning as the
+ *     op's `params` (fixtures/k3/head.json), plus the launch scalars the manifest launch supplies.
+ *     Each entry point validates shapes on the host, then launches its kernel through layer 1 from
+ *     the library's own pinned code object (kern_mx.hsaco).
+ *
+ * Every function returns KERN_OK (0) or a kern_status; kern_last_error() gives the message for the
+ * calling thread. Device pointers must be on the device current on the calling thread. Calls are
+ * asynchronous on `stream` (NULL = the null stream).
+ */
+#ifndef KERN_AMD_H
+#define KERN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, grouped by who acts, as crates/kern-runtime/src/error.rs:5-67 groups its Error. */
+typedef enum kern_status {
+  KERN_OK = 0,
+  KERN_ERR_MANIFEST = 1,        /* manifest inconsistency found past verification (error.rs:7-11) */
+  KERN_ERR_KERNEL_ARTIFACT = 2, /* code object missing/unreadable, sha256 mismatch, param layout (error.rs:13-17) */
+  KERN_ERR_WEIGHT_ARTIFACT = 3, /* weight bytes not as the op needs them (error.rs:19-23) */
+  KERN_ERR_API = 4,             /* caller broke the contract: bad shape, null pointer, unknown name (error.rs:25-30) */
+  KERN_ERR_DOMAIN = 6,          /* an input value outside the op's domain (error.rs:38-42) */
+  KERN_ERR_CALL = 7,            /* one launch of a program failed; message carries the call context (error.rs:44-51) */
+  KERN_ERR_HIP = 8              /* a HIP runtime call failed (error.rs:53-55, the CUDA variant) */
+} kern_status;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kern_last_error(void);
+
+/* ------------------------------------------------------------------------------------------------
+ * Module layer (replaces kern-runtime's CUDA driver calls)
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct kern_module_s* kern_module;
+typedef struct kern_function_s* kern_function;
+typedef struct kern_graph_s* kern_graph;
+
+/* Lower-case hex SHA-256 of `len` bytes into out[65]. (cubin.rs:62-109 pins modules by this digest) */
+int kern_sha256_hex(const void* data, size_t len, char out[65]);
+
+/* Load a code object image on the current device after checking its SHA-256 against `sha256_hex`
+ * (64 hex chars; NULL skips the check). Replaces cuModuleLoadData in cubin.rs:226-263 and the
+ * pinning of cubin.rs:70-109. */
+int kern_module_load(const void* image, size_t len, const char* sha256_hex, kern_module* out);
+int kern_module_unload(kern_module mod);
+
+/* Resolve an entry (cuModuleGetFunction, compile.rs:313-445). */
+int kern_module_function(kern_module mod, const char* entry, kern_function* out);
+
+/* Explicit kernel-argument sizes of an entry, read from the code object's AMDGPU metadata (our own
+ * build), in order: the analog of cuFuncGetParamInfo used by the ABI check in compile.rs:385-415.
+ * Writes up to `cap` sizes; *n gets the count. */
+int kern_function_param_sizes(kern_function fn, uint32_t* sizes, int cap, int* n);
+
+/* The same sizes read from a code object image in host memory, without a device (a manifest's
+ * launches can be checked against an artifact before any GPU is touched). */
+int kern_code_object_param_sizes(const void* image, size_t len, const char* entry, uint32_t* sizes, int cap,
+                                 int* n);
+
+/* The ABI check itself: KERN_ERR_KERNEL_ARTIFACT unless the entry's explicit arguments are exactly
+ * `n` arguments of the given byte sizes (pointer 8, i32/f32 4, i64 8, bytes<n> n). */
+int kern_function_check_params(kern_function fn, const uint32_t* sizes, int n);
+
+/* Launch with a packed kernel-argument buffer laid out per the AMDGPU kernarg ABI (each argument at
+ * its natural alignment). Replaces cuLaunchKernelEx (exec.rs:726-821). */
+int kern_launch(kern_function fn, const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
+                void* stream, const void* kernargs, size_t kernargs_size);
+
+/* hipGraph capture of everything enqueued on `stream` between begin and end, then replay
+ * (exec.rs:489-548 record, :644-654 enqueue_captured). */
+int kern_graph_begin(void* stream);
+int kern_graph_end(void* stream, kern_graph* out);
+int kern_graph_launch(kern_graph g, void* stream);
+int kern_graph_destroy(kern_graph g);
+
+/* ------------------------------------------------------------------------------------------------
+ * Op layer. The library loads its code object kern_mx.hsaco (next to libkern_amd.so unless
+ * kern_init names another path) on first use per device and checks the SHA-256 it was built with.
+ * ------------------------------------------------------------------------------------------------ */
+
+/* Optional explicit init: path of kern_mx.hsaco (NULL = next to the library). */
+int kern_init(const char* code_object_path);
+/* SHA-256 the library pins its code object to (64 hex chars). */
+const char* kern_code_object_sha256(void);
+
+/* moe_quant (fixtures/k3/head.json:25057; rule tools/trtllm-bmm/probe.py:38-43):
+ * in bf16 x[T][K], out u8 q[T][K] (e4m3), out u8 sf[T][K/32] (ue8m0, linear), i32 T; launch i32 K.
+ * Per 32-block: scale = clamp(floor(log2 amax) - 8 + 127, 0, 254), codes RNE-saturating e4m3.
+ * K % 32 == 0. */
+int kern_moe_quant(const void* x, void* q, void* sf, int32_t tokens, int32_t K, void* stream);
+
+/* k3_moe_w_shuffle (head.json:26358; derive program head.json:28670): in u8 raw [E][rows][row_bytes],
+ * out u8 repacked (same size), i32 rows, i32 row_bytes, i32 gated; launch i32 E.
+ * rows % 16 == 0, row_bytes % 256 == 0 (K % 512 == 0). */
+int kern_moe_w_shuffle(const void* raw, void* out, int32_t experts, int32_t rows, int32_t row_bytes,
+                       int32_t gated, void* stream);
+
+/* k3_moe_sf_shuffle (head.json:26413): in u8 raw [E][rows][sf_cols], out u8 repacked, i32 rows,
+ * i32 sf_cols, i32 gated; launch i32 E. rows % 16 == 0, sf_cols % 16 == 0. */
+int kern_moe_sf_shuffle(const void* raw, void* out, int32_t experts, int32_t rows, int32_t sf_cols,
+                        int32_t gated, void* stream);
+
+/* moe_routing (head.json:25117; tables of tools/kernels/abi/trtllm_bmm.py:19-27, :50-60):
+ * in i32 topk_idx[tokens][topk] -> out counts[2*local_experts], cta_batch[ctas], cta_limit[ctas],
+ * num_non_exiting[1], total_padded[1], route_map[ctas*128], exp2perm[tokens*topk].
+ * ctas = local_experts + ceil(tokens*topk/128) bounds the slots. local_experts <= 512. */
+int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_t* cta_batch, int32_t* cta_limit,
+                     int32_t* num_non_exiting, int32_t* total_padded, int32_t* route_map, int32_t* exp2perm,
+                     int32_t tokens, int32_t topk, int32_t local_start, int32_t local_experts, void* stream);
+
+/* trtllm_bmm_bf16_mxe2m1_mxe4m3 = moe_fc2 (head.json:25683; interface trtllm_bmm.py:19-27):
+ * a u8 [E][m][k/2] repacked MXFP4, sf_a repacked, b u8 [rows][k] e4m3, sf_b (R128c4 over rows when
+ * sf_b_r128c4, else linear [rows][k/32]), c bf16 [rows][m], num_non_exiting, total_padded, cta_batch,
+ * cta_limit; launch: m, k, ctas (grid.y, the manifest's E + ceil(tokens*topk/128)), and dbg (NULL or
+ * f32 [rows][m] pre-rounding accumulators). m % 256 == 0, k % 512 == 0. */
+int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c,
+                                       const int32_t* num_non_exiting, const int32_t* total_padded,
+                                       const int32_t* cta_batch, const int32_t* cta_limit, int32_t m, int32_t k,
+                                       int32_t ctas, int32_t sf_b_r128c4, float* dbg, void* stream);
+
+/* trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 = moe_fc1 (head.json:25459): a (gated repack), sf_a, b u8 [T][k]
+ * e4m3, sf_b linear [T][k/32], c u8 [rows][m/2] e4m3, sf_c u8 R128c4 over rows x (m/2)/32, route_map,
+ * alpha f32[E], beta f32[E], num_non_exiting, total_padded, cta_batch, cta_limit; launch m, k, ctas,
+ * dbg (NULL or f32 [rows][3][m/2] = gate acc, up acc, SiTU-GLU value). m % 256 == 0, k % 512 == 0. */
+int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c,
+                                         void* sf_c, const int32_t* route_map, const float* alpha,
+                                         const float* beta, const int32_t* num_non_exiting,
+                                         const int32_t* total_padded, const int32_t* cta_batch,
+                                         const int32_t* cta_limit, int32_t m, int32_t k, int32_t ctas, float* dbg,
+                                         void* stream);
+
+/* Dense e4m3-output mode of the FC1 family (no gate, per-tensor output scale), the prefill GEMM:
+ * c[t][n] = e4m3_rne_sat(acc[t][n] * d_scale[0]); a/sf_a repacked [m][k], b u8 [M][k], sf_b linear,
+ * c u8 [M][m], d_scale f32[1] on the device; dbg NULL or f32 [M][m]. */
+int kern_mxfp4_gemm_e4m3(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c,
+                         const float* d_scale, int32_t M, int32_t m, int32_t k, float* dbg, void* stream);
+
+/* Dense bf16-output mode of the FC2 family: c bf16 [M][m]. */
+int kern_mxfp4_gemm_bf16(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c, int32_t M,
+                         int32_t m, int32_t k, float* dbg, void* stream);
+
+/* mxfp4_gemv_bf16 (new op; the W4A16 decode, no reference counterpart): in bf16 x[M][K], in u8 w
+ * repacked [N][K/2], in u8 w_sf repacked, out bf16 y[M][N], i32 M (1..16); launch N, K.
+ * N % 16 == 0, K % 512 == 0. */
+int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_sf, void* y, int32_t M, int32_t N, int32_t K,
+                         void* stream);
+
+/* Seeded synthetic bytes: out[i] = lo + splitmix64_i(seed) % span (crates/kern-test/src/workload.rs:11-26). */
+int kern_fill_random_u8(void* out, int64_t n, uint64_t seed, int32_t lo, int32_t span, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

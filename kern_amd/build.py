@@ -1,0 +1,115 @@
+"""Build the gfx950 code object and the C-ABI library in-tree.
+
+    python -m kern_amd.build
+
+1. `hipcc --genco --offload-arch=gfx950` compiles kern_amd/csrc/kern_mx.hip to kern_amd/lib/kern_mx.hsaco.
+2. Its SHA-256 is compiled into libkern_amd.so (the library refuses any other code object) and written
+   to kernel_index/kern_mx.toml with the entries and their kernel-argument sizes, the way kern's
+   kernel_index pins its modules by digest (tools/kernels/index.py:1-19).
+3. The host side (capi.cpp, no device code) is compiled with g++ against the HIP runtime.
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIBDIR = os.path.join(HERE, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HSACO = os.path.join(LIBDIR, "kern_mx.hsaco")
+LIB = os.path.join(LIBDIR, "libkern_amd.so")
+ARCH = "gfx950"
+
+# hipcc flags for device code: packed-fp32 VALU ops stay off (they have given wrong results on these boxes)
+DEVICE_FLAGS = ["-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+                "-packed-fp32-ops"]
+
+ENTRIES = {
+    # entry: (launch params as the op JSON in kernel_index/ declares them)
+    "kern_mx_quant_bf16": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "i32"],
+    "kern_mx_w_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
+    "kern_mx_sf_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
+    "kern_mx_gemv_bf16": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32", "i32",
+                          "i32"],
+    "kern_mx_bmm_fc2": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
+                        "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "i32",
+                        "out buffer<f32>"],
+    "kern_mx_bmm_fc1": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<u8>",
+                        "out buffer<u8>", "in buffer<i32>", "in buffer<f32>", "in buffer<f32>", "in buffer<i32>",
+                        "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "out buffer<f32>"],
+    "kern_mx_gemm_e4m3": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<u8>",
+                          "in buffer<f32>", "i32", "i32", "i32", "out buffer<f32>"],
+    "kern_mx_gemm_bf16": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
+                          "i32", "i32", "i32", "out buffer<f32>"],
+    "kern_mx_routing": ["in buffer<i32>"] + ["out buffer<i32>"] * 7 + ["i32"] * 4,
+    "kern_mx_fill_random_u8": ["out buffer<u8>", "i64", "u64", "i32", "i32"],
+}
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+def build_code_object() -> str:
+    os.makedirs(LIBDIR, exist_ok=True)
+    tmp = HSACO + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", "--no-gpu-bundle-output", *DEVICE_FLAGS, os.path.join(CSRC, "kern_mx.hip"),
+          "-o", tmp])
+    os.replace(tmp, HSACO)
+    with open(HSACO, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def build_library(sha: str) -> None:
+    tmp = LIB + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function",
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DKERN_MX_SHA256="{sha}"',
+          os.path.join(CSRC, "capi.cpp"), "-o", tmp, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+          "-ldl"])
+    os.replace(tmp, LIB)
+
+
+def write_index(sha: str) -> None:
+    idx = os.path.join(ROOT, "kernel_index")
+    os.makedirs(idx, exist_ok=True)
+    lines = [
+        "# gfx950 code object of the MXFP4 matmul path, pinned by sha256 (written by kern_amd/build.py).",
+        "# Each [[entry]] lists the launch params a manifest op declares for it; the runtime checks them",
+        "# against the code object's own kernel-argument metadata before the first launch.",
+        "[module]",
+        'name = "kern_mx"',
+        'kind = "hsaco"',
+        f'arch = "{ARCH}"',
+        'source = "kern_amd/lib/kern_mx.hsaco"',
+        f'sha256 = "{sha}"',
+        "",
+    ]
+    for name, params in ENTRIES.items():
+        lines += ["[[entry]]", f'name = "{name}"', "params = [" + ", ".join(f'"{p}"' for p in params) + "]", ""]
+    with open(os.path.join(idx, "kern_mx.toml"), "w") as f:
+        f.write("\n".join(lines))
+
+
+def build_oracle() -> None:
+    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
+
+
+def build(oracle: bool = True) -> str:
+    sha = build_code_object()
+    build_library(sha)
+    write_index(sha)
+    if oracle:
+        build_oracle()
+    return sha
+
+
+if __name__ == "__main__":
+    print(build(oracle="--no-oracle" not in sys.argv))

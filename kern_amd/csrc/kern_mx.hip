@@ -1,0 +1,658 @@
+// gfx950 kernels of the MXFP4 matmul path. Built into one code object (kern_mx.hsaco) whose entries
+// take flat kernel arguments in the order of their manifest launch `params`; the C ABI in capi.cpp
+// launches them with hipModuleLaunchKernel from that sha256-pinned object.
+//
+// Data layouts in HBM (all byte offsets; E experts, m weight rows, K reduction length):
+//   raw MXFP4 weights   u8 [E][m][K/2], element 2j in the low nibble        (probe.py:28)
+//   raw scales          u8 [E][m][K/32] e8m0                                 (probe.py:31)
+//   repacked weights    per expert, 1 KiB fragment ((R/16)*(K/128) + k/128); lane L = 16*((k%128)/32) + R%16
+//                       owns the 16 bytes at L*16 = k in [128*kt + 32*(L/16), +32) of row R: exactly the
+//                       fp4 A-operand of V_MFMA_SCALE_F32_16X16X128_F8F6F4 for lane L.
+//   repacked scales     per expert, 256 B fragment ((R/16)*(K/512) + k/512); lane L owns a dword whose byte j
+//                       is the scale of row R, k-block 16*kg + 4*j + L/16 (MFMA scale operand, OPSEL = j).
+//   gated (FC1) rows    repacked row R holds raw row: quad (R%16)/4 of group R/16 is gate n, gate n+1, up n,
+//                       up n+1 (n = 8*(R/16) + 2*((R%16)/4)); gate = rows [m/2, m) (w1), up = [0, m/2) (w3).
+//   activations         e4m3 u8 [rows][K], scales linear u8 [rows][K/32] or R128c4 (cublas.rs:396-400)
+#include "mx_device.h"
+
+template <int V>
+struct IC { static constexpr int value = V; };
+
+// ====================================================================================== quantizer
+// op moe_quant (fixtures/k3/head.json:25057): in bf16 x[T][K], out u8 q[T][K], out u8 sf[T][K/32], i32 T,
+// launch i32 K. One thread per 32-element block; grid ceil(T*K/32 / 256), block 256 (the reference grid).
+extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint16_t* __restrict__ x,
+                                                                     uint8_t* __restrict__ q,
+                                                                     uint8_t* __restrict__ sf, int T, int K) {
+  const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nblk = (int64_t)T * (K / 32);
+  if (blk >= nblk) return;
+  const v4u* src = reinterpret_cast<const v4u*>(x + blk * 32);
+  v4u v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = __builtin_nontemporal_load(src + i);
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = v[i][j];
+      uint32_t lo = (w << 16) & 0x7fffffffu, hi = w & 0x7fff0000u;
+      amax = max(amax, max(lo, hi));
+    }
+  const uint32_t sc = mx_scale_code(amax);
+  v4u out[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t packed[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w0 = v[i][2 * h], w1 = v[i][2 * h + 1];
+      uint32_t c0 = mx_elem_code(w0 << 16, sc), c1 = mx_elem_code(w0 & 0xffff0000u, sc);
+      uint32_t c2 = mx_elem_code(w1 << 16, sc), c3 = mx_elem_code(w1 & 0xffff0000u, sc);
+      packed[h] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    }
+    out[i / 2][2 * (i % 2)] = packed[0];
+    out[i / 2][2 * (i % 2) + 1] = packed[1];
+  }
+  v4u* dst = reinterpret_cast<v4u*>(q + blk * 32);
+  dst[0] = out[0];
+  dst[1] = out[1];
+  sf[blk] = (uint8_t)sc;
+}
+
+// ====================================================================================== repack
+// derive op k3_moe_w_shuffle (head.json:26358): in u8 raw, out u8 shuffled, i32 rows, i32 row_bytes,
+// i32 gated; launch prepends i32 E. One thread per 16-byte lane slot of the output; grid
+// E*rows*row_bytes/16/256, block 256.
+KERN_DEV int64_t w_src_row(int64_t R, int64_t rows, int gated) {
+  if (!gated) return R;
+  int64_t j = R & 3;
+  int64_t n = 8 * (R >> 4) + 2 * ((R & 15) >> 2) + (j & 1);
+  return j < 2 ? (rows >> 1) + n : n;
+}
+
+extern "C" __global__ __launch_bounds__(256) void kern_mx_w_shuffle(const uint8_t* __restrict__ raw,
+                                                                    uint8_t* __restrict__ out, int E, int rows,
+                                                                    int row_bytes, int gated) {
+  const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte output slot
+  const int64_t KT = row_bytes / 64;
+  const int64_t per_e = (int64_t)rows * row_bytes / 16;
+  if (slot >= per_e * E) return;
+  const int64_t e = slot / per_e;
+  const int64_t s = slot - e * per_e;
+  const int64_t frag = s >> 6, L = s & 63;
+  const int64_t rg = frag / KT, kt = frag - rg * KT;
+  const int64_t R = rg * 16 + (L & 15);
+  const int64_t src = (e * rows + w_src_row(R, rows, gated)) * row_bytes + kt * 64 + (L >> 4) * 16;
+  const v4u val = *reinterpret_cast<const v4u*>(raw + src);
+  reinterpret_cast<v4u*>(out)[slot] = val;
+}
+
+// derive op k3_moe_sf_shuffle (head.json:26413): in u8 raw, out u8 shuffled, i32 rows, i32 sf_cols,
+// i32 gated; launch prepends i32 E. One thread per output dword; grid E*rows*sf_cols/4/256, block 256.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_sf_shuffle(const uint8_t* __restrict__ raw,
+                                                                     uint8_t* __restrict__ out, int E, int rows,
+                                                                     int sf_cols, int gated) {
+  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;  // output dword
+  const int64_t KG = sf_cols / 16;
+  const int64_t per_e = (int64_t)rows * sf_cols / 4;
+  if (d >= per_e * E) return;
+  const int64_t e = d / per_e;
+  const int64_t s = d - e * per_e;
+  const int64_t frag = s >> 6, L = s & 63;
+  const int64_t rg = frag / KG, kg = frag - rg * KG;
+  const int64_t R = rg * 16 + (L & 15);
+  const uint8_t* src = raw + (e * rows + w_src_row(R, rows, gated)) * sf_cols + kg * 16 + (L >> 4);
+  uint32_t v = (uint32_t)src[0] | ((uint32_t)src[4] << 8) | ((uint32_t)src[8] << 16) | ((uint32_t)src[12] << 24);
+  reinterpret_cast<uint32_t*>(out)[d] = v;
+}
+
+// ====================================================================================== decode GEMV
+// op mxfp4_gemv_bf16 (new; the W4A16 decode of BASELINE configs 1-2): in bf16 x[M][K], in u8 w (repacked,
+// non-gated) [N][K/2], in u8 w_sf (repacked), out bf16 y[M][N], i32 M, launch i32 N, i32 K.
+// Grid N/16, block 256: one 16-row group per workgroup, the four waves split the K groups (512 wide)
+// and reduce through LDS. fp4 is decoded with its scale by V_CVT_SCALEF32_PK_BF16_FP4 and multiplied on
+// V_MFMA_F32_16X16X32_BF16 (tokens are the 16 B columns; columns >= M are zero).
+extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16(const uint16_t* __restrict__ x,
+                                                                    const uint8_t* __restrict__ w,
+                                                                    const uint8_t* __restrict__ wsf,
+                                                                    uint16_t* __restrict__ y, int M, int N, int K) {
+  __shared__ v4f red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = blockIdx.x;
+  const int KT = K >> 7, KG = K >> 9;
+  const int g0 = (KG * wave) >> 2, g1 = (KG * (wave + 1)) >> 2;
+  const int c = lane & 15, grp = lane >> 4;
+  const bool live = c < M;
+  const v4u* wf = reinterpret_cast<const v4u*>(w + ((int64_t)rg * KT) * 1024) + lane;
+  const uint32_t* sfp = reinterpret_cast<const uint32_t*>(wsf + ((int64_t)rg * KG) * 256) + lane;
+  const uint16_t* xr = x + (int64_t)(live ? c : 0) * K + grp * 32;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kg = g0; kg < g1; ++kg) {
+    v4u wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wv[j] = __builtin_nontemporal_load(wf + (kg * 4 + j) * 64);
+    const uint32_t sdw = sfp[kg * 64];
+    v4u xv[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4u* xp = reinterpret_cast<const v4u*>(xr + (kg * 4 + j) * 128);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[j][i] = live ? xp[i] : (v4u){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s = e8m0_to_f32((sdw >> (8 * j)) & 0xffu);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // A: 8 fp4 of this lane's row, k = 32*grp + 8*i .. +8 (dword i of the fragment slot)
+        const uint32_t wd = wv[j][i];
+        v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
+        v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
+        v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
+        v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
+        v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        v8bf b = __builtin_bit_cast(v8bf, xv[j][i]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+      }
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    v4f s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    if (live) {
+      // lane (c, grp) holds rows 4*grp + i of the group for token c
+      const int n0 = rg * 16 + grp * 4;
+      uint32_t lo = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
+      uint32_t hi = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
+      uint2* dst = reinterpret_cast<uint2*>(y + (int64_t)c * N + n0);
+      *dst = make_uint2(lo, hi);
+    }
+  }
+}
+
+// ====================================================================================== block-scaled GEMM
+// One workgroup computes a 128-row (token/slot) x 256-row (weight) tile with 4 waves in a 2x2 grid; each
+// wave owns 64 x 128 = 4 x 8 tiles of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (A = fp4 weights, B = e4m3
+// activations, e8m0 scales in-instruction). K advances 128 per step through double-buffered LDS:
+//   W: 16 fragments of 1 KiB, copied verbatim (the repacked layout is the MFMA operand layout);
+//   X: 128 rows x 128 B, 16-byte chunk j of row t stored at t*128 + ((j ^ ((t>>1)&7)) << 4) so that both
+//      the row-wise writes and the fragment reads (rows 0..15, one chunk) touch 16 distinct bank groups;
+//   scales once per 512 of K: W fragments verbatim, X as dwords [k-tile][row].
+enum { MODE_FC2 = 0, MODE_FC1 = 1, MODE_PT = 2, MODE_DENSE_BF16 = 3 };
+
+struct BmmArgs {
+  const uint8_t* a;      // repacked weights [E][m][k/2]
+  const uint8_t* sf_a;   // repacked scales
+  const uint8_t* b;      // e4m3 activations
+  const uint8_t* sf_b;   // activation scales
+  void* c;               // output
+  uint8_t* sf_c;         // FC1 output scales (R128c4)
+  const int* route_map;  // FC1 gather
+  const float* alpha;
+  const float* beta;
+  const int* num_non_exiting;
+  const int* cta_batch;
+  const int* cta_limit;
+  const float* d_scale;  // PT
+  float* dbg;            // optional f32 debug output
+  int m, k, rows;        // rows: dense M
+  int sf_b_r128c4;
+};
+
+#define BT 128
+#define BN 256
+#define LDS_W (BN * 64)
+#define LDS_X (BT * 128)
+#define LDS_SW (16 * 256)
+#define LDS_SX (4 * BT * 4)
+
+template <int MODE>
+KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wt = wave >> 1, wn = wave & 1;
+  const int gx = A.m / BN;
+  // XCD-aware linearisation: consecutive workgroups land on different XCDs (round robin over 8); give
+  // each XCD a contiguous run of tiles so that its L2 sees the reuse.
+  const int total = gridDim.x * gridDim.y;
+  int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  const int nx = lin % gx, slot = lin / gx;
+
+  int expert = 0, row0 = slot * BT, limit;
+  if (MODE == MODE_PT || MODE == MODE_DENSE_BF16) {
+    if (row0 >= A.rows) return;
+    limit = min(A.rows, row0 + BT);
+  } else {
+    if (slot >= A.num_non_exiting[0]) return;
+    expert = A.cta_batch[slot];
+    limit = A.cta_limit[slot];
+  }
+  const int valid = limit - row0;  // 1..128
+  const int K = A.k, KT = K >> 7, KG = K >> 9;
+  const int m = A.m;
+
+  uint8_t* ldsW[2] = {lds, lds + LDS_W};
+  uint8_t* ldsX[2] = {lds + 2 * LDS_W, lds + 2 * LDS_W + LDS_X};
+  uint8_t* ldsSW[2] = {lds + 2 * (LDS_W + LDS_X), lds + 2 * (LDS_W + LDS_X) + LDS_SW};
+  uint8_t* ldsSX[2] = {lds + 2 * (LDS_W + LDS_X + LDS_SW), lds + 2 * (LDS_W + LDS_X + LDS_SW) + LDS_SX};
+
+  // global sources
+  const int rg0 = (nx * BN) >> 4;  // first 16-row group of this tile
+  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)rg0 * KT) * 1024;
+  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)rg0 * KG) * 256;
+  // X rows this thread stages: t = tid/8 + 32*i (i = 0..3), chunk j = tid%8
+  const int xj = tid & 7;
+  int64_t xrow[4];
+  bool xok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = (tid >> 3) + 32 * i;
+    xok[i] = t < valid;
+    int64_t r = row0 + t;
+    if (MODE == MODE_FC1) r = xok[i] ? A.route_map[row0 + t] : 0;
+    xrow[i] = xok[i] ? r : 0;
+  }
+  // X scale staging: thread -> (row t = tid & 127, k-tile pair q = tid >> 7): two dwords each
+  const int st = tid & 127, sq = tid >> 7;
+  int64_t srow;
+  bool sok = st < valid;
+  {
+    int64_t r = row0 + st;
+    if (MODE == MODE_FC1) r = sok ? A.route_map[row0 + st] : 0;
+    srow = sok ? r : 0;
+  }
+
+  v4u gw[4], gx4[4];
+  v4u gsw;
+  uint32_t gsx[2];
+
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = i * 4 + (tid >> 6);  // fragment (row group) 0..15
+      gw[i] = *(reinterpret_cast<const v4u*>(wbase + ((int64_t)f * KT + kt) * 1024) + lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (xok[i])
+        gx4[i] = *reinterpret_cast<const v4u*>(A.b + xrow[i] * K + (int64_t)kt * 128 + xj * 16);
+    }
+  };
+  auto load_scales = [&](int kg) {
+    gsw = *reinterpret_cast<const v4u*>(sbase + ((int64_t)(tid >> 4) * KG + kg) * 256 + (tid & 15) * 16);
+    if (sok) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kt = kg * 4 + sq * 2 + h;
+        int64_t off;
+        if (A.sf_b_r128c4) {
+          const int64_t kb4 = K >> 7;  // ceil(kblocks/4) with K % 128 == 0
+          off = 512 * ((srow >> 7) * kb4 + kt) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
+        } else {
+          off = srow * (K >> 5) + kt * 4;
+        }
+        gsx[h] = *reinterpret_cast<const uint32_t*>(A.sf_b + off);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = i * 4 + (tid >> 6);
+      *reinterpret_cast<v4u*>(ldsW[buf] + f * 1024 + lane * 16) = gw[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = (tid >> 3) + 32 * i;
+      if (xok[i]) *reinterpret_cast<v4u*>(ldsX[buf] + t * 128 + ((xj ^ ((t >> 1) & 7)) << 4)) = gx4[i];
+    }
+  };
+  auto store_scales = [&](int buf) {
+    *reinterpret_cast<v4u*>(ldsSW[buf] + tid * 16) = gsw;
+    if (sok) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) reinterpret_cast<uint32_t*>(ldsSX[buf])[(sq * 2 + h) * BT + st] = gsx[h];
+    }
+  };
+
+  v4f acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  // number of live 16-row token subtiles for this wave
+  const int live_ts = min(4, max(0, (valid - wt * 64 + 15) >> 4));
+  const int c = lane & 15, g = lane >> 4;
+
+  load_scales(0);
+  load_tile(0);
+  store_scales(0);
+  store_tile(0);
+  __syncthreads();
+
+  auto step = [&](int kg, auto Jc) {
+    constexpr int j = decltype(Jc)::value;
+    const int sb = kg & 1;
+    const int kt = kg * 4 + j;
+    const int buf = kt & 1;
+    const bool more = kt + 1 < KT;
+    if (more) load_tile(kt + 1);
+    if (j == 3 && more) load_scales(kg + 1);
+    uint32_t swd[8];
+#pragma unroll
+    for (int rs = 0; rs < 8; ++rs)
+      swd[rs] = reinterpret_cast<const uint32_t*>(ldsSW[sb] + (wn * 8 + rs) * 256)[lane];
+    v4i wa[8];
+#pragma unroll
+    for (int rs = 0; rs < 8; ++rs)
+      wa[rs] = *reinterpret_cast<const v4i*>(ldsW[buf] + (wn * 8 + rs) * 1024 + lane * 16);
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      if (ts < live_ts) {
+        const int t = wt * 64 + ts * 16 + c;
+        const uint8_t* xr = ldsX[buf] + t * 128;
+        const int sw = (t >> 1) & 7;
+        v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
+        v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
+        v8i xb = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        const uint32_t sx = reinterpret_cast<const uint32_t*>(ldsSX[sb])[j * BT + t] >> (8 * g);
+#pragma unroll
+        for (int rs = 0; rs < 8; ++rs) {
+          v8i wb = {wa[rs][0], wa[rs][1], wa[rs][2], wa[rs][3], 0, 0, 0, 0};
+          acc[ts][rs] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb, acc[ts][rs], 4, 0, j,
+                                                                          (int)swd[rs], 0, (int)sx);
+        }
+      }
+    }
+    if (more) {
+      if (j == 3) store_scales(sb ^ 1);
+      store_tile(buf ^ 1);
+    }
+    __syncthreads();
+  };
+  for (int kg = 0; kg < KG; ++kg) {
+    step(kg, IC<0>{});
+    step(kg, IC<1>{});
+    step(kg, IC<2>{});
+    step(kg, IC<3>{});
+  }
+
+  // ---- epilogue: lane (c, g) of tile (ts, rs) holds weight rows 16*rs + 4*g + i, token row c
+  const int wrow0 = nx * BN + wn * 128;  // first weight row of this wave
+  if (MODE == MODE_FC2 || MODE == MODE_DENSE_BF16) {
+    uint16_t* C = reinterpret_cast<uint16_t*>(A.c);
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const int t = wt * 64 + ts * 16 + c;
+      if (t < valid) {
+        const int64_t p = row0 + t;
+#pragma unroll
+        for (int rs = 0; rs < 8; ++rs) {
+          const int n = wrow0 + rs * 16 + g * 4;
+          const v4f v = acc[ts][rs];
+          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
+          uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+          uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+          *reinterpret_cast<uint2*>(C + p * m + n) = make_uint2(lo, hi);
+        }
+      }
+    }
+  } else if (MODE == MODE_PT) {
+    uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
+    const float ds = A.d_scale[0];
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const int t = wt * 64 + ts * 16 + c;
+      if (t < valid) {
+        const int64_t p = row0 + t;
+#pragma unroll
+        for (int rs = 0; rs < 8; ++rs) {
+          const int n = wrow0 + rs * 16 + g * 4;
+          const v4f v = acc[ts][rs];
+          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
+          uint32_t o = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o |= e4m3_rne(__float_as_uint(v[i] * ds), 0) << (8 * i);
+          *reinterpret_cast<uint32_t*>(C + p * m + n) = o;
+        }
+      }
+    }
+  } else {  // MODE_FC1: gated SiTU-GLU, e4m3 + ue8m0 block-32 (R128c4) output
+    uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
+    const int half = m >> 1;
+    const float al = A.alpha[expert], be = A.beta[expert];
+    const int ncol0 = (nx * BN + wn * 128) >> 1;  // first output column of this wave (64 of them)
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const int t = wt * 64 + ts * 16 + c;
+      // h for 8 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
+      float h[8][2];
+#pragma unroll
+      for (int rs = 0; rs < 8; ++rs) {
+        const v4f v = acc[ts][rs];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float gg = v[i], uu = v[i + 2];
+          const float sg = 1.0f / (1.0f + __expf(-gg));
+          h[rs][i] = al * tanhf(gg / al) * sg * be * tanhf(uu / be);
+        }
+      }
+      const bool ok = t < valid;
+      const int64_t p = row0 + t;
+      if (ok && A.dbg) {
+#pragma unroll
+        for (int rs = 0; rs < 8; ++rs)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int n = ncol0 + 8 * rs + 2 * g + i;
+            A.dbg[(p * 3 + 0) * half + n] = acc[ts][rs][i];
+            A.dbg[(p * 3 + 1) * half + n] = acc[ts][rs][i + 2];
+            A.dbg[(p * 3 + 2) * half + n] = h[rs][i];
+          }
+      }
+      // two 32-column blocks: subtiles 0-3 and 4-7
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk) {
+        uint32_t amax = 0;
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[bk * 4 + rs][i]) & 0x7fffffffu);
+        amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
+        amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
+        const uint32_t sc = mx_scale_code(amax);
+        if (ok) {
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs) {
+            const int n = ncol0 + 8 * (bk * 4 + rs) + 2 * g;
+            uint32_t o = mx_elem_code(__float_as_uint(h[bk * 4 + rs][0]), sc) |
+                         (mx_elem_code(__float_as_uint(h[bk * 4 + rs][1]), sc) << 8);
+            *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
+          }
+          if (g == 0) {
+            const int blk = (ncol0 >> 5) + bk;
+            const int64_t kb4 = ((half >> 5) + 3) >> 2;
+            const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
+            A.sf_c[off] = (uint8_t)sc;
+          }
+        }
+      }
+    }
+  }
+}
+
+#define BMM_LDS_BYTES (2 * (LDS_W + LDS_X + LDS_SW + LDS_SX))
+
+// op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
+// a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
+// cta_batch, cta_limit; launch adds i32 m, i32 k, i32 sf_b_r128c4, f32* dbg (may be null).
+// Grid [m/256, slots, 1], block 256; slot y >= num_non_exiting[0] exits.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2(
+    const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
+    const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
+    int sf_b_r128c4, float* dbg) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BmmArgs A = {};
+  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
+  A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
+  A.m = m; A.k = k; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
+  (void)total_padded;
+  bmm_tile<MODE_FC2>(A, lds);
+}
+
+// op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
+// c u8 [padded][m/2], sf_c u8 R128c4, route_map, alpha, beta, num_non_exiting, total_padded, cta_batch,
+// cta_limit; launch adds i32 m, i32 k, f32* dbg. Grid [m/256, slots, 1], block 256.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc1(
+    const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
+    const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
+    const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, float* dbg) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BmmArgs A = {};
+  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.sf_c = sf_c; A.route_map = route_map;
+  A.alpha = alpha; A.beta = beta;
+  A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
+  A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  (void)total_padded;
+  bmm_tile<MODE_FC1>(A, lds);
+}
+
+// Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).
+// a, sf_a, b [M][k], sf_b linear, c u8 [M][m], d_scale f32[1], i32 M; launch adds i32 m, i32 k, f32* dbg.
+// Grid [m/256, ceil(M/128), 1], block 256.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_e4m3(const uint8_t* a, const uint8_t* sf_a,
+                                                                    const uint8_t* b, const uint8_t* sf_b,
+                                                                    uint8_t* c, const float* d_scale, int M, int m,
+                                                                    int k, float* dbg) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BmmArgs A = {};
+  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.d_scale = d_scale;
+  A.m = m; A.k = k; A.rows = M; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  bmm_tile<MODE_PT>(A, lds);
+}
+
+// Dense bf16-output mode of the FC2 family (one batch, no routing tables).
+extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_bf16(const uint8_t* a, const uint8_t* sf_a,
+                                                                    const uint8_t* b, const uint8_t* sf_b,
+                                                                    uint16_t* c, int M, int m, int k, float* dbg) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BmmArgs A = {};
+  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
+  A.m = m; A.k = k; A.rows = M; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  bmm_tile<MODE_DENSE_BF16>(A, lds);
+}
+
+// ====================================================================================== routing
+// op moe_routing (head.json:25117): in i32 topk_idx[T][topk]; out counts [2E], cta_batch, cta_limit,
+// num_non_exiting[1], total_padded[1], route_map, exp2perm [T*topk]; launch adds i32 T, i32 topk,
+// i32 local_start, i32 E_local (<= 512). One workgroup of 1024 threads; rows of one expert in ascending
+// expanded index, each expert padded to 128-row CTA slots (tables as tools/kernels/abi/trtllm_bmm.py:19-27).
+#define ROUTE_EMAX 512
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
+    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
+    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+  __shared__ int cnt[ROUTE_EMAX];   // per-expert count, then the running rank base
+  __shared__ int off[ROUTE_EMAX];   // per-expert first slot
+  __shared__ int wtab[16][ROUTE_EMAX];  // per-wave count of each expert in the current round
+  __shared__ int total_slots;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = T * topk;
+  for (int e = tid; e < E_local; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += 1024) {
+    const int e = topk_idx[i] - local_start;
+    if (e >= 0 && e < E_local) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int s = 0;
+    for (int e = 0; e < E_local; ++e) {
+      off[e] = s;
+      s += (cnt[e] + 127) >> 7;
+    }
+    total_slots = s;
+    num_non_exiting[0] = s;
+    total_padded[0] = s * 128;
+  }
+  __syncthreads();
+  const int S = total_slots;
+  for (int e = tid; e < E_local; e += 1024) {
+    counts[e] = cnt[e];
+    counts[E_local + e] = off[e];
+    const int ns = (cnt[e] + 127) >> 7;
+    for (int s = 0; s < ns; ++s) {
+      cta_batch[off[e] + s] = e;
+      cta_limit[off[e] + s] = min((off[e] + s + 1) * 128, off[e] * 128 + cnt[e]);
+    }
+  }
+  for (int p = tid; p < S * 128; p += 1024) route_map[p] = -1;
+  __syncthreads();
+  for (int e = tid; e < E_local; e += 1024) cnt[e] = 0;
+  for (int base = 0; base < n; base += 1024) {
+    for (int q = tid; q < 16 * ROUTE_EMAX; q += 1024) (&wtab[0][0])[q] = 0;
+    __syncthreads();
+    const int i = base + tid;
+    int e = -1;
+    if (i < n) {
+      e = topk_idx[i] - local_start;
+      if (e < 0 || e >= E_local) e = -1;
+    }
+    // rank among lower lanes of this wave holding the same expert
+    unsigned long long same = 0;
+    unsigned long long pending = __ballot(e >= 0);
+    while (pending) {
+      const int leader = __ffsll((long long)pending) - 1;
+      const int le = __shfl(e, leader);
+      const unsigned long long mk = __ballot(e == le);
+      if (e == le) same = mk;
+      pending &= ~mk;
+    }
+    const int rank = __popcll(same & ((1ull << lane) - 1ull));
+    if (e >= 0 && rank == 0) wtab[wave][e] = __popcll(same);
+    __syncthreads();
+    if (e >= 0) {
+      int before = 0;
+      for (int w2 = 0; w2 < wave; ++w2) before += wtab[w2][e];
+      const int p = off[e] * 128 + cnt[e] + before + rank;
+      exp2perm[i] = p;
+      route_map[p] = i / topk;
+    } else if (i < n) {
+      exp2perm[i] = -1;
+    }
+    __syncthreads();
+    for (int e2 = tid; e2 < E_local; e2 += 1024) {
+      int add = 0;
+      for (int w2 = 0; w2 < 16; ++w2) add += wtab[w2][e2];
+      cnt[e2] += add;
+    }
+    __syncthreads();
+  }
+}
+
+// ====================================================================================== workload fills
+// Synthetic seeded inputs (splitmix64 stream, crates/kern-test/src/workload.rs:11-26):
+// out[i] = lo + draw_i % span.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_fill_random_u8(uint8_t* __restrict__ out, int64_t n,
+                                                                         uint64_t seed, int lo, int span) {
+  int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+  if (i >= n) return;
+  if (i + 16 <= n) {
+    v4u v;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t d = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        d |= (uint32_t)((lo + (int)(splitmix64_at(seed, i + 4 * w + b) % (uint64_t)span)) & 0xff) << (8 * b);
+      v[w] = d;
+    }
+    *reinterpret_cast<v4u*>(out + i) = v;
+  } else {
+    for (int64_t j = i; j < n; ++j) out[j] = (uint8_t)(lo + (int)(splitmix64_at(seed, j) % (uint64_t)span));
+  }
+}

@@ -1,0 +1,107 @@
+// Device-side element codecs and helpers shared by the gfx950 kernels.
+//
+// The arithmetic here is integer-exact and matches the CPU oracle bit for bit:
+//   * e2m1: sign = bit 3, magnitude table {0, .5, 1, 1.5, 2, 3, 4, 6}   (tools/trtllm-bmm/probe.py:24-31)
+//   * e8m0: 2^(c-127), 255 = NaN                                         (crates/kern-manifest/src/values.rs:18-24)
+//   * e4m3fn: round-to-nearest-even, saturating to +-448, NaN -> 0x7f|sign
+//   * MXFP8 block scale: clamp(floor(log2 amax) - 8 + 127, 0, 254)       (probe.py:38-43 floor rule)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+#define KERN_DEV static __device__ __forceinline__
+
+KERN_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+// round-to-nearest-even f32 -> bf16 bits (NaN stays a quiet NaN)
+KERN_DEV uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// RNE of mant >> s for s in [1, 31]
+KERN_DEV uint32_t rne_shr(uint32_t mant, uint32_t s) {
+  uint32_t q = mant >> s;
+  uint32_t rem = mant & ((1u << s) - 1u);
+  uint32_t half = 1u << (s - 1u);
+  return q + ((rem > half) | ((rem == half) & (q & 1u)));
+}
+
+// e4m3fn code of (f32 with bits `bits`) * 2^shift, round-to-nearest-even, saturating.
+KERN_DEV uint32_t e4m3_rne(uint32_t bits, int shift) {
+  uint32_t sign = (bits >> 24) & 0x80u;
+  uint32_t a = bits & 0x7fffffffu;
+  if (a >= 0x7f800000u) return sign | (a == 0x7f800000u ? 0x7eu : 0x7fu);
+  if (a == 0) return sign;
+  int E = (int)(a >> 23);
+  uint32_t mant;
+  int e;
+  if (E != 0) {
+    mant = (a & 0x7fffffu) | 0x800000u;
+    e = E - 127;
+  } else {  // f32 subnormal: normalise so bit 23 is set
+    uint32_t m = a & 0x7fffffu;
+    int lz = __clz(m) - 8;
+    mant = m << lz;
+    e = -126 - lz;
+  }
+  e += shift;
+  if (e >= -6) {
+    uint32_t r = rne_shr(mant, 20);  // 8..16
+    int ef = e + 7 + (int)(r >> 4);
+    uint32_t code = ((uint32_t)ef << 3) | (r & 7u);
+    if (ef > 15) code = 0x7eu;
+    code = code > 0x7eu ? 0x7eu : code;
+    return sign | code;
+  }
+  int s = 14 - e;  // >= 21
+  uint32_t q = s >= 32 ? 0u : rne_shr(mant, (uint32_t)s);
+  return sign | q;
+}
+
+// floor(log2 |x|) for a finite nonzero f32 given |bits|
+KERN_DEV int floor_log2_abs(uint32_t a) {
+  int E = (int)(a >> 23);
+  if (E > 0) return E - 127;
+  return (31 - __clz(a & 0x7fffffu)) - 149;
+}
+
+// MXFP8 scale code for a block whose largest |bits| is amax (0x7f800000+ means non-finite present)
+KERN_DEV uint32_t mx_scale_code(uint32_t amax_bits) {
+  if (amax_bits >= 0x7f800000u) return 255u;
+  if (amax_bits == 0) return 0u;
+  int c = floor_log2_abs(amax_bits) - 8 + 127;
+  c = c < 0 ? 0 : c;
+  c = c > 254 ? 254 : c;
+  return (uint32_t)c;
+}
+
+// element code of an f32 value in a block with scale code `sc`
+KERN_DEV uint32_t mx_elem_code(uint32_t bits, uint32_t sc) {
+  if (sc == 255u) return ((bits >> 24) & 0x80u) | 0x7fu;
+  return e4m3_rne(bits, 127 - (int)sc);
+}
+
+// f32 value 2^(code-127) (code 0 is the subnormal 2^-127, 255 is NaN)
+KERN_DEV float e8m0_to_f32(uint32_t code) {
+  if (code == 0u) return __uint_as_float(0x00400000u);
+  if (code == 255u) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float(code << 23);
+}
+
+// splitmix64 i-th draw of a stream (crates/kern-test/src/workload.rs:18-24)
+KERN_DEV uint64_t splitmix64_at(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1ull) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}

@@ -1,0 +1,229 @@
+"""Python mirror of the path's manifest ops over the C ABI (include/kern_amd.h).
+
+Each function has the name, parameter order and meaning of a manifest op of kern's MXFP4 matmul
+path (fixtures/k3/head.json ops `moe_quant`, `k3_moe_w_shuffle`, `k3_moe_sf_shuffle`, `moe_routing`,
+`moe_fc1` = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3, `moe_fc2` = trtllm_bmm_bf16_mxe2m1_mxe4m3), followed by the
+scalars the op's launch supplies as keywords. Buffers are torch tensors on a HIP device; the call is
+enqueued on torch's current stream. A contract violation raises KernError with the library's message,
+as the reference runtime returns Error::Api (crates/kern-runtime/src/error.rs:25-30). There is no CPU
+fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libkern_amd.so")
+HSACO_PATH = os.path.join(HERE, "lib", "kern_mx.hsaco")
+
+STATUS = {0: "ok", 1: "manifest", 2: "kernel artifact", 3: "weight artifact", 4: "caller contract", 6: "domain",
+          7: "call", 8: "hip"}
+
+
+class KernError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+
+_SIGS = {
+    "kern_moe_quant": [P, P, P, I32, I32, P],
+    "kern_moe_w_shuffle": [P, P, I32, I32, I32, I32, P],
+    "kern_moe_sf_shuffle": [P, P, I32, I32, I32, I32, P],
+    "kern_moe_routing": [P] * 8 + [I32] * 4 + [P],
+    "kern_trtllm_bmm_bf16_mxe2m1_mxe4m3": [P] * 9 + [I32, I32, I32, I32, P, P],
+    "kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3": [P] * 13 + [I32, I32, I32, P, P],
+    "kern_mxfp4_gemm_e4m3": [P] * 6 + [I32, I32, I32, P, P],
+    "kern_mxfp4_gemm_bf16": [P] * 5 + [I32, I32, I32, P, P],
+    "kern_mxfp4_gemv_bf16": [P] * 4 + [I32, I32, I32, P],
+    "kern_fill_random_u8": [P, I64, ctypes.c_uint64, I32, I32, P],
+    "kern_init": [ctypes.c_char_p],
+    "kern_sha256_hex": [P, ctypes.c_size_t, ctypes.c_char_p],
+    "kern_code_object_param_sizes": [P, ctypes.c_size_t, ctypes.c_char_p, P, ctypes.c_int, P],
+    "kern_module_load": [P, ctypes.c_size_t, ctypes.c_char_p, P],
+    "kern_module_unload": [P],
+    "kern_module_function": [P, ctypes.c_char_p, P],
+    "kern_function_param_sizes": [P, P, ctypes.c_int, P],
+    "kern_function_check_params": [P, P, ctypes.c_int],
+    "kern_launch": [P, P, P, ctypes.c_uint32, P, P, ctypes.c_size_t],
+    "kern_graph_begin": [P],
+    "kern_graph_end": [P, P],
+    "kern_graph_launch": [P, P],
+    "kern_graph_destroy": [P],
+}
+
+
+def lib() -> ctypes.CDLL:
+    """The C-ABI library; raises if it has not been built (python -m kern_amd.build)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise KernError(2, f"{LIB_PATH} is missing: build it with `python -m kern_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        L.kern_last_error.restype = ctypes.c_char_p
+        L.kern_last_error.argtypes = []
+        L.kern_code_object_sha256.restype = ctypes.c_char_p
+        L.kern_code_object_sha256.argtypes = []
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise KernError(rc, lib().kern_last_error().decode())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t, name, dtype=None, numel=None):
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        raise KernError(4, f"{name}: expected a torch.Tensor")
+    if not t.is_cuda:
+        raise KernError(4, f"{name}: must be a device tensor")
+    if not t.is_contiguous():
+        raise KernError(4, f"{name}: must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise KernError(4, f"{name}: dtype {t.dtype}, expected {dtype}")
+    if numel is not None and t.numel() < numel:
+        raise KernError(4, f"{name}: {t.numel()} elements, need at least {numel}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+u8, i32, f32, bf16 = torch.uint8, torch.int32, torch.float32, torch.bfloat16
+
+
+def code_object_sha256() -> str:
+    return lib().kern_code_object_sha256().decode()
+
+
+# ------------------------------------------------------------------------------------------- ops
+
+def moe_quant(x, q, sf, tokens, *, K):
+    """moe_quant(in bf16 x[T,K], out u8 q[T,K], out u8 sf[T,K/32], i32 tokens) — head.json:25057."""
+    check(lib().kern_moe_quant(_ptr(x, "x", bf16, tokens * K), _ptr(q, "q", u8, tokens * K),
+                               _ptr(sf, "sf", u8, tokens * K // 32), tokens, K, _stream()))
+
+
+def k3_moe_w_shuffle(raw, out, rows, row_bytes, gated, *, experts):
+    """k3_moe_w_shuffle(in u8 raw, out u8 shuffled, i32 rows, i32 row_bytes, i32 gated) — head.json:26358."""
+    n = experts * rows * row_bytes
+    check(lib().kern_moe_w_shuffle(_ptr(raw, "raw", u8, n), _ptr(out, "out", u8, n), experts, rows, row_bytes,
+                                   int(gated), _stream()))
+
+
+def k3_moe_sf_shuffle(raw, out, rows, sf_cols, gated, *, experts):
+    """k3_moe_sf_shuffle(in u8 raw, out u8 shuffled, i32 rows, i32 sf_cols, i32 gated) — head.json:26413."""
+    n = experts * rows * sf_cols
+    check(lib().kern_moe_sf_shuffle(_ptr(raw, "raw", u8, n), _ptr(out, "out", u8, n), experts, rows, sf_cols,
+                                    int(gated), _stream()))
+
+
+def ctas_bound(tokens, topk, experts, tile=128):
+    """The op's grid.y: experts + ceil(tokens*topk/tile) (tools/kernels/abi/trtllm_bmm.py:58-60)."""
+    return experts + -(-tokens * topk // tile)
+
+
+def moe_routing(topk_idx, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, *,
+                tokens, topk, local_start, local_experts):
+    """moe_routing(in i32 topk_idx, out counts, cta_batch, cta_limit, num_non_exiting, total_padded,
+    route_map, exp2perm) — head.json:25117."""
+    ctas = ctas_bound(tokens, topk, local_experts)
+    check(lib().kern_moe_routing(
+        _ptr(topk_idx, "topk_idx", i32, tokens * topk), _ptr(counts, "counts", i32, 2 * local_experts),
+        _ptr(cta_batch, "cta_batch", i32, ctas), _ptr(cta_limit, "cta_limit", i32, ctas),
+        _ptr(num_non_exiting, "num_non_exiting", i32, 1), _ptr(total_padded, "total_padded", i32, 1),
+        _ptr(route_map, "route_map", i32, ctas * 128), _ptr(exp2perm, "exp2perm", i32, tokens * topk),
+        tokens, topk, local_start, local_experts, _stream()))
+
+
+def trtllm_bmm_bf16_mxe2m1_mxe4m3(a, sf_a, b, sf_b, c, num_non_exiting, total_padded, cta_batch, cta_limit, *, m, k,
+                                  ctas, sf_b_r128c4=True, dbg=None):
+    """moe_fc2 (head.json:25683): bf16 c[rows, m] = MXFP8 b[rows, k] x MXFP4 a[e, m, k]^T per CTA slot."""
+    rows = ctas * 128
+    check(lib().kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(
+        _ptr(a, "a", u8), _ptr(sf_a, "sf_a", u8), _ptr(b, "b", u8, rows * k), _ptr(sf_b, "sf_b", u8),
+        _ptr(c, "c", bf16, rows * m), _ptr(num_non_exiting, "num_non_exiting", i32, 1),
+        _ptr(total_padded, "total_padded", i32, 1), _ptr(cta_batch, "cta_batch", i32, ctas),
+        _ptr(cta_limit, "cta_limit", i32, ctas), m, k, ctas, int(bool(sf_b_r128c4)),
+        _ptr(dbg, "dbg", f32, rows * m), _stream()))
+
+
+def trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(a, sf_a, b, sf_b, c, sf_c, route_map, alpha, beta, num_non_exiting,
+                                    total_padded, cta_batch, cta_limit, *, m, k, ctas, dbg=None):
+    """moe_fc1 (head.json:25459): e4m3 c[rows, m/2] + ue8m0 sf_c = MXFP8(SiTU-GLU(b[route_map] x a^T))."""
+    rows = ctas * 128
+    check(lib().kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(
+        _ptr(a, "a", u8), _ptr(sf_a, "sf_a", u8), _ptr(b, "b", u8), _ptr(sf_b, "sf_b", u8),
+        _ptr(c, "c", u8, rows * m // 2), _ptr(sf_c, "sf_c", u8), _ptr(route_map, "route_map", i32, rows),
+        _ptr(alpha, "alpha", f32), _ptr(beta, "beta", f32), _ptr(num_non_exiting, "num_non_exiting", i32, 1),
+        _ptr(total_padded, "total_padded", i32, 1), _ptr(cta_batch, "cta_batch", i32, ctas),
+        _ptr(cta_limit, "cta_limit", i32, ctas), m, k, ctas, _ptr(dbg, "dbg", f32, rows * 3 * (m // 2)),
+        _stream()))
+
+
+def mxfp4_gemm_e4m3(a, sf_a, b, sf_b, c, d_scale, *, M, m, k, dbg=None):
+    """Dense e4m3-output mode: c[M, m] = e4m3(MXFP8 b[M, k] x MXFP4 a[m, k]^T * d_scale)."""
+    check(lib().kern_mxfp4_gemm_e4m3(
+        _ptr(a, "a", u8, m * k // 2), _ptr(sf_a, "sf_a", u8, m * k // 32), _ptr(b, "b", u8, M * k),
+        _ptr(sf_b, "sf_b", u8, M * k // 32), _ptr(c, "c", u8, M * m), _ptr(d_scale, "d_scale", f32, 1), M, m, k,
+        _ptr(dbg, "dbg", f32, M * m), _stream()))
+
+
+def mxfp4_gemm_bf16(a, sf_a, b, sf_b, c, *, M, m, k, dbg=None):
+    """Dense bf16-output mode: c[M, m] = bf16(MXFP8 b[M, k] x MXFP4 a[m, k]^T)."""
+    check(lib().kern_mxfp4_gemm_bf16(
+        _ptr(a, "a", u8, m * k // 2), _ptr(sf_a, "sf_a", u8, m * k // 32), _ptr(b, "b", u8, M * k),
+        _ptr(sf_b, "sf_b", u8, M * k // 32), _ptr(c, "c", bf16, M * m), M, m, k, _ptr(dbg, "dbg", f32, M * m),
+        _stream()))
+
+
+def mxfp4_gemv_bf16(x, w, w_sf, y, M, *, N, K):
+    """W4A16 decode: y[M, N] = bf16(x[M, K] x deq(w)[N, K]^T), 1 <= M <= 16."""
+    check(lib().kern_mxfp4_gemv_bf16(
+        _ptr(x, "x", bf16, M * K), _ptr(w, "w", u8, N * K // 2), _ptr(w_sf, "w_sf", u8, N * K // 32),
+        _ptr(y, "y", bf16, M * N), M, N, K, _stream()))
+
+
+def fill_random_u8(out, seed, lo=0, span=256):
+    """out[i] = lo + splitmix64_i(seed) % span (crates/kern-test/src/workload.rs:11-26)."""
+    check(lib().kern_fill_random_u8(_ptr(out, "out", u8), out.numel(), seed & (2**64 - 1), lo, span, _stream()))
+
+
+# ------------------------------------------------------------------------------------- helpers
+
+def quantize_mxfp8(x: torch.Tensor):
+    """Allocate and run moe_quant over a bf16 [T, K] tensor -> (q u8 [T, K], sf u8 [T, K/32])."""
+    T, K = x.shape
+    q = torch.empty((T, K), dtype=u8, device=x.device)
+    sf = torch.empty((T, K // 32), dtype=u8, device=x.device)
+    moe_quant(x, q, sf, T, K=K)
+    return q, sf
+
+
+def repack_weights(raw_w: torch.Tensor, raw_sf: torch.Tensor, gated: bool = False):
+    """Run the two derive ops over raw [E, rows, K/2] nibbles and [E, rows, K/32] scales."""
+    if raw_w.dim() == 2:
+        raw_w, raw_sf = raw_w.unsqueeze(0), raw_sf.unsqueeze(0)
+    E, rows, rb = raw_w.shape
+    w = torch.empty_like(raw_w)
+    sf = torch.empty_like(raw_sf)
+    k3_moe_w_shuffle(raw_w, w, rows, rb, gated, experts=E)
+    k3_moe_sf_shuffle(raw_sf, sf, rows, raw_sf.shape[2], gated, experts=E)
+    return w, sf

@@ -1,0 +1,272 @@
+"""GPU parity of every op of the path against the CPU oracle, through the C ABI.
+
+Bit-exact: quantizer, repack, routing tables, the fill generator, e4m3/ue8m0 epilogue codes (given the
+kernel's own pre-quantisation values). Tolerance (north star): GEMM outputs within max-abs
+1e-2*||row||_inf and relative Frobenius 2e-3 of the fp32-accumulate oracle on exactly dequantised
+operands.
+"""
+import numpy as np
+import pytest
+
+from kern_amd import workload as wl
+from tests._util import assert_gemm_close, bf16_to_f32, r128c4_offsets, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from kern_amd import ops
+
+    ops.lib()
+    return ops
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+# --------------------------------------------------------------------------------------- fills
+
+def test_fill_random_matches_host_stream(ops):
+    n = (1 << 20) + 7
+    for seed, lo, span in [(1, 0, 256), (12345, 122, 11), (2**63 + 5, 124, 7)]:
+        out = torch.empty(n, dtype=torch.uint8, device="cuda")
+        ops.fill_random_u8(out, seed, lo, span)
+        _sync()
+        np.testing.assert_array_equal(to_np(out), wl.uniform_bytes(seed, n, lo, span))
+
+
+# --------------------------------------------------------------------------------------- quantizer
+
+def _special_rows(K):
+    rows = []
+    f = np.zeros((8, K), np.float32)
+    f[0] = 0.0                                   # all-zero blocks -> scale code 0
+    f[1] = 1.0                                   # power-of-two amax
+    f[2, ::32] = 1.875                           # amax mantissa 1.875 -> 480 before saturation
+    f[2, 1::32] = 1.75 / 2**6                    # tiny next to it
+    f[3] = np.float32(2.0**-130)                 # bf16 subnormals
+    f[4] = np.linspace(-3e38, 3e38, K).astype(np.float32)  # extreme magnitudes
+    f[5] = np.float32(448.0)
+    f[5, 1::32] = 464.0                          # the RNE midpoint above 448
+    f[6] = np.tile(np.float32([1.0, 1.0625, 1.125, 1.1875, 1.03125, 1.09375]), K)[:K]  # ties
+    f[7, 0] = np.inf
+    f[7, 40] = np.nan
+    f[7, 64:96] = -np.inf
+    rows.append(wl.f32_to_bf16_bits(f))
+    return np.concatenate(rows)
+
+
+@pytest.mark.parametrize("T,K", [(64, 1024), (4096, 7168)])
+def test_quant_bitexact(ops, oracle, T, K):
+    x = wl.activations_bf16(7 + T, T, K, outlier_frac=0.01)
+    x[:8] = _special_rows(K)
+    xd = to_dev(x)
+    q, sf = ops.quantize_mxfp8(xd)
+    _sync()
+    q_ref, sf_ref = oracle.quant_mxfp8(x)
+    np.testing.assert_array_equal(to_np(sf), sf_ref)
+    np.testing.assert_array_equal(to_np(q), q_ref)
+
+
+# --------------------------------------------------------------------------------------- repack
+
+@pytest.mark.parametrize("gated", [0, 1])
+def test_repack_bitexact(ops, oracle, gated):
+    E, rows, K = 3, 64, 1024
+    w, sf = wl.mxfp4_weights(11 + gated, E, rows, K, 118, 136)
+    wd, sfd = ops.repack_weights(to_dev(w), to_dev(sf), gated=bool(gated))
+    _sync()
+    np.testing.assert_array_equal(to_np(wd).reshape(-1), oracle.w_shuffle(w, E, rows, K // 2, gated).reshape(-1))
+    np.testing.assert_array_equal(to_np(sfd).reshape(-1), oracle.sf_shuffle(sf, E, rows, K // 32, gated).reshape(-1))
+
+
+# --------------------------------------------------------------------------------------- decode GEMV
+
+@pytest.mark.parametrize("M,N,K,lo,hi", [(8, 512, 1024, 124, 130), (1, 18432, 7168, 122, 132),
+                                         (4, 18432, 7168, 122, 132), (16, 18432, 7168, 122, 132),
+                                         (3, 1024, 2048, 100, 150)])
+def test_gemv_w4a16(ops, oracle, M, N, K, lo, hi):
+    x = wl.activations_bf16(100 + M, M, K)
+    w, sf = wl.mxfp4_weights(200 + M, 1, N, K, lo, hi)
+    wp, sfp = ops.repack_weights(to_dev(w[0]), to_dev(sf[0]))
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ops.mxfp4_gemv_bf16(to_dev(x), wp, sfp, y, M, N=N, K=K)
+    _sync()
+    _, yf = oracle.gemv_w4a16(x, w[0], sf[0])
+    assert_gemm_close(bf16_to_f32(to_np(y)), yf, f"gemv M={M}")
+
+
+# --------------------------------------------------------------------------------------- closed-form KAT
+
+def test_gemm_closed_form_kat(ops):
+    """Row i of the e4m3 activations is one 1.0 at column 7i mod K; weights are in {-2..2}; scales are powers
+    of two per (row, block) — so out[i, n] = w[n, col(i)] * 2^(ea(i,b) + ew(n,b)) exactly
+    (the design of crates/kern-runtime/tests/mxfp8_gemm.rs:40-95)."""
+    M, N, K = 256, 512, 1024
+    col = (np.arange(M) * 7) % K
+    a = np.zeros((M, K), np.uint8)
+    a[np.arange(M), col] = 0x38                     # e4m3 1.0
+    wv = ((np.arange(N)[:, None] + np.arange(K)[None, :]) % 5) - 2
+    code = {-2: 0xC, -1: 0xA, 0: 0x0, 1: 0x2, 2: 0x4}  # e2m1 nibbles
+    nib = np.vectorize(code.get)(wv).astype(np.uint8)
+    w = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    ea = lambda r, b: ((r + b) % 3) - 1
+    ew = lambda r, b: ((3 * r + 2 * b) % 5) - 2
+    rr, bb = np.meshgrid(np.arange(M), np.arange(K // 32), indexing="ij")
+    sa = (127 + ea(rr, bb)).astype(np.uint8)
+    rn, bn = np.meshgrid(np.arange(N), np.arange(K // 32), indexing="ij")
+    sw = (127 + ew(rn, bn)).astype(np.uint8)
+    wp, swp = ops.repack_weights(to_dev(w), to_dev(sw))
+    c = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ops.mxfp4_gemm_bf16(wp, swp, to_dev(a), to_dev(sa), c, M=M, m=N, k=K)
+    _sync()
+    b = col // 32
+    expect = wv[:, col].T * np.exp2(ea(np.arange(M), b)[:, None] + ew(np.arange(N)[None, :], b[:, None]))
+    np.testing.assert_array_equal(bf16_to_f32(to_np(c)), expect.astype(np.float32))
+
+
+# --------------------------------------------------------------------------------------- dense e4m3 (config 3 mode)
+
+@pytest.mark.parametrize("M,m,k", [(300, 512, 1024), (4096, 2048, 7168)])
+def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
+    x = wl.activations_bf16(31, M, k, outlier_frac=0.01)
+    w, sf = wl.mxfp4_weights(32, 1, m, k, 122, 132)
+    xd = to_dev(x)
+    q, qs = ops.quantize_mxfp8(xd)
+    wp, sfp = ops.repack_weights(to_dev(w[0]), to_dev(sf[0]))
+    d_scale = 1.0 / 64.0
+    ds = torch.tensor([d_scale], dtype=torch.float32, device="cuda")
+    c = torch.empty((M, m), dtype=torch.uint8, device="cuda")
+    dbg = torch.empty((M, m), dtype=torch.float32, device="cuda")
+    ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c, ds, M=M, m=m, k=k, dbg=dbg)
+    _sync()
+    acc = to_np(dbg)
+    rows = slice(None) if M <= 512 else np.r_[0:128, 1900:2000, M - 70:M]
+    qn, qsn = to_np(q), to_np(qs)
+    ref_c, ref_acc = oracle.gemm_e4m3_pt(to_np(wp), to_np(sfp), qn[rows], qsn[rows], m, k, d_scale)
+    assert_gemm_close(acc[rows], ref_acc, "prefill acc")
+    # the epilogue cast is bit-exact given the kernel's own accumulator
+    np.testing.assert_array_equal(to_np(c), oracle.e4m3_from_f32(acc * np.float32(d_scale)))
+
+
+# --------------------------------------------------------------------------------------- routing
+
+@pytest.mark.parametrize("T,E,k,start,local", [(512, 256, 8, 0, 256), (37, 16, 4, 4, 8), (1, 8, 2, 0, 8),
+                                               (300, 224, 16, 56, 56), (2048, 64, 6, 0, 64)])
+def test_routing_bitexact(ops, oracle, T, E, k, start, local):
+    ids = wl.topk_ids(T * 31 + E, T, E, k)
+    ctas = ops.ctas_bound(T, k, local)
+    ref = oracle.routing(ids, start, local, ctas_cap=ctas)
+    dev = {n: torch.full((s,), -7, dtype=torch.int32, device="cuda") for n, s in
+           [("counts", 2 * local), ("cta_batch", ctas), ("cta_limit", ctas), ("num_non_exiting", 1),
+            ("total_padded", 1), ("route_map", ctas * 128), ("exp2perm", T * k)]}
+    ops.moe_routing(to_dev(ids), dev["counts"], dev["cta_batch"], dev["cta_limit"], dev["num_non_exiting"],
+                    dev["total_padded"], dev["route_map"], dev["exp2perm"], tokens=T, topk=k, local_start=start,
+                    local_experts=local)
+    _sync()
+    S = int(ref["num_non_exiting"][0])
+    assert int(to_np(dev["num_non_exiting"])[0]) == S
+    assert int(to_np(dev["total_padded"])[0]) == S * 128
+    np.testing.assert_array_equal(to_np(dev["counts"]), ref["counts"])
+    np.testing.assert_array_equal(to_np(dev["cta_batch"])[:S], ref["cta_batch"][:S])
+    np.testing.assert_array_equal(to_np(dev["cta_limit"])[:S], ref["cta_limit"][:S])
+    np.testing.assert_array_equal(to_np(dev["route_map"])[:S * 128], ref["route_map"][:S * 128])
+    np.testing.assert_array_equal(to_np(dev["exp2perm"]), ref["exp2perm"].reshape(-1))
+
+
+# --------------------------------------------------------------------------------------- grouped FC1 / FC2
+
+def _route(ops, oracle, ids, local_start, local):
+    T, k = ids.shape
+    ctas = ops.ctas_bound(T, k, local)
+    tabs = oracle.routing(ids, local_start, local, ctas_cap=ctas)
+    dev = {n: to_dev(v.reshape(-1)) for n, v in tabs.items()}
+    return ctas, tabs, dev
+
+
+@pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 4096, 7168)])
+def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
+    ids = wl.topk_ids(5 + T, T, E, k)
+    ctas, tabs, dev = _route(ops, oracle, ids, 0, E)
+    x = wl.activations_bf16(6 + T, T, K)
+    w, sf = wl.mxfp4_weights(8 + T, E, m, K, 119, 124)
+    q, qs = ops.quantize_mxfp8(to_dev(x))
+    wp, sfp = ops.repack_weights(to_dev(w), to_dev(sf), gated=True)
+    alpha = np.full(E, 4.0, np.float32) + np.arange(E, dtype=np.float32) * 0.01
+    beta = np.full(E, 25.0, np.float32)
+    rows = ctas * 128
+    half = m // 2
+    c = torch.zeros((rows, half), dtype=torch.uint8, device="cuda")
+    sf_c = torch.zeros(oracle.r128c4_size(rows, half // 32), dtype=torch.uint8, device="cuda")
+    dbg = torch.zeros((rows, 3, half), dtype=torch.float32, device="cuda")
+    ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(wp, sfp, q, qs, c, sf_c, dev["route_map"], to_dev(alpha), to_dev(beta),
+                                        dev["num_non_exiting"], dev["total_padded"], dev["cta_batch"],
+                                        dev["cta_limit"], m=m, k=K, ctas=ctas, dbg=dbg)
+    _sync()
+    S = int(tabs["num_non_exiting"][0])
+    # check a bounded sample of slots against the oracle (the whole thing at small shapes)
+    slots = list(range(S)) if S <= 16 else list(range(0, S, max(1, S // 12)))[:12]
+    sub = dict(tabs)
+    sub["num_non_exiting"] = np.array([len(slots)], np.int32)
+    sub["cta_batch"] = tabs["cta_batch"][slots]
+    sub["cta_limit"] = (tabs["cta_limit"][slots] - np.array(slots, np.int32) * 128
+                        + np.arange(len(slots), dtype=np.int32) * 128).astype(np.int32)
+    perm = np.concatenate([np.arange(s * 128, s * 128 + 128) for s in slots])
+    sub["route_map"] = tabs["route_map"][perm]
+    ref_c, ref_sfc, ref_dbg = oracle.fc1(to_np(wp), to_np(sfp), to_np(q), to_np(qs), sub, alpha, beta, m, K,
+                                         len(slots) * 128)
+    g = to_np(dbg)[perm]
+    valid = np.concatenate([np.arange(128) < (tabs["cta_limit"][s] - s * 128) for s in slots])
+    assert_gemm_close(g[valid, 0], ref_dbg[valid, 0], "fc1 gate acc")
+    assert_gemm_close(g[valid, 1], ref_dbg[valid, 1], "fc1 up acc")
+    # SiTU-GLU on the kernel's accumulators, against the formula (probe.py:46-47)
+    h_ref = np.vectorize(oracle.situ, otypes=[np.float32])(g[valid, 0], g[valid, 1],
+                                                           alpha[np.repeat(sub["cta_batch"], 128)[valid]][:, None],
+                                                           beta[np.repeat(sub["cta_batch"], 128)[valid]][:, None])
+    np.testing.assert_allclose(g[valid, 2], h_ref, rtol=2e-5, atol=1e-6)
+    # e4m3 codes and ue8m0 scales: bit-exact against the oracle quantiser on the kernel's own h
+    cn = to_np(c)[perm][valid]
+    sfn = to_np(sf_c)
+    qref, sref = oracle.quant_blocks(g[valid, 2])
+    np.testing.assert_array_equal(cn, qref)
+    pv = perm[valid]
+    offs = np.array([[oracle.r128c4_offset(int(p), b, half // 32) for b in range(half // 32)] for p in pv])
+    np.testing.assert_array_equal(sfn[offs], sref)
+
+
+@pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 7168, 2048)])
+def test_fc2_bf16(ops, oracle, T, E, k, m, K):
+    ids = wl.topk_ids(9 + T, T, E, k)
+    ctas, tabs, dev = _route(ops, oracle, ids, 0, E)
+    rows = ctas * 128
+    # activations in permuted row order (what FC1 writes): e4m3 codes and R128c4 scales
+    xb = wl.activations_bf16(10 + T, rows, K)
+    q_lin, qs_lin = oracle.quant_mxfp8(xb)
+    qs_r = np.zeros(oracle.r128c4_size(rows, K // 32), np.uint8)
+    qs_r[r128c4_offsets(rows, K // 32)] = qs_lin
+    w, sf = wl.mxfp4_weights(12 + T, E, m, K, 118, 126)
+    wp, sfp = ops.repack_weights(to_dev(w), to_dev(sf))
+    c = torch.zeros((rows, m), dtype=torch.bfloat16, device="cuda")
+    ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(wp, sfp, to_dev(q_lin), to_dev(qs_r), c, dev["num_non_exiting"],
+                                      dev["total_padded"], dev["cta_batch"], dev["cta_limit"], m=m, k=K, ctas=ctas,
+                                      sf_b_r128c4=True)
+    _sync()
+    S = int(tabs["num_non_exiting"][0])
+    slots = list(range(S)) if S <= 16 else list(range(0, S, max(1, S // 10)))[:10]
+    wpn, sfpn = to_np(wp), to_np(sfp)
+    got = bf16_to_f32(to_np(c))
+    for s in slots:
+        e, lim = int(tabs["cta_batch"][s]), int(tabs["cta_limit"][s])
+        r0 = s * 128
+        sub = {"num_non_exiting": np.array([1], np.int32), "cta_batch": np.array([0], np.int32),
+               "cta_limit": np.array([lim - r0], np.int32)}
+        per_e = m * K // 2
+        _, acc = oracle.fc2(wpn.reshape(-1)[e * per_e:(e + 1) * per_e], sfpn.reshape(-1)[e * per_e // 16:(e + 1) * per_e // 16],
+                            q_lin[r0:r0 + 128], qs_lin[r0:r0 + 128], False, sub, m, K)
+        assert_gemm_close(got[r0:lim], acc[:lim - r0], f"fc2 slot {s}")
