@@ -1,0 +1,271 @@
+"""Benchmark of the MXFP4 matmul path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemm|decode]
+
+Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
+
+* step = one pass of config 3 over resident inputs: bf16 activations [4096, 7168] (N(0,1), 1% outliers x20)
+  quantised on the GPU to MXFP8 (op moe_quant), then the MXFP4 x MXFP8 GEMM against repacked weights
+  [2048, 7168] with the e4m3 per-tensor-scaled epilogue. `value` = 2*M*N*K / (wall time of a step) in
+  TFLOP/s, so the quantiser's time counts against it.
+* `roofline` = the GEMM kernel alone: algorithmic FLOPs per launch / its average launch time, measured
+  with HIP events on the stream it runs on, against the dense MXFP4 MFMA peak (10.1 PFLOP/s); the
+  fraction against the FP8 MFMA rate (5.0 PFLOP/s, the rate of an fp8-operand scaled MFMA) is given too.
+* `decode` = config 2 at M=1: W4A16 GEMV over [18432, 7168] MXFP4 weights, rotating over enough weight
+  copies (> 256 MB, the Infinity Cache) that every launch streams its weights from HBM; GB/s of
+  algorithmic bytes against the 8 TB/s HBM peak.
+* `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on a bounded
+  sample of the same GEMM (its first rows), in the headline unit.
+* `traffic` comes from committed rocprofv3 --pmc summaries (profiles/traffic.json), null without one.
+
+Inputs are seeded synthetic data (splitmix64, kern_amd/workload.py), generated once before timing.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_MXFP4_TFLOPS = 10100.0  # MI355X dense MXFP4/MXFP6 MFMA, published
+PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, published (fp8-operand scaled MFMA rate)
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
+
+# config 3 (prefill GEMM) and config 2 (decode GEMV) shapes, BASELINE.json configs[2] / configs[1]
+PM, PN, PK = 4096, 2048, 7168
+DN, DK = 18432, 7168
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--only", choices=["gemm", "decode"], default=None,
+                    help="run one leg only (for profiling); the JSON line then carries that leg")
+    ap.add_argument("--decode-m", type=int, default=1)
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def dev_from_np(a, torch):
+    import numpy as np
+
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(a).cuda()
+
+
+def timed_loop(torch, stream, fn_step, kernel_fn, steps, warmup):
+    """Run `warmup` untimed steps, then `steps` timed ones. fn_step(i) enqueues one step; kernel_fn(i)
+    enqueues the dominant kernel of that step, bracketed by events. Returns (ms per step, avg kernel ms)."""
+    for i in range(warmup):
+        fn_step(i, None)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    t0.record(stream)
+    for i in range(steps):
+        fn_step(i, evs[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - w0) * 1e3
+    ms = t0.elapsed_time(t1)
+    kms = [a.elapsed_time(b) for a, b in evs]
+    kms.sort()
+    return ms / steps, sum(kms) / len(kms), kms[len(kms) // 2], wall / steps
+
+
+def load_traffic(kernel):
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        d = json.load(f)
+    v = d.get(kernel)
+    return None if v is None else v.get("bytes_per_launch")
+
+
+def bench_gemm(torch, ops, wl, stream, steps, warmup):
+    import numpy as np
+
+    log(f"config 3: generating inputs M={PM} N={PN} K={PK}")
+    x = dev_from_np(wl.activations_bf16(3, PM, PK, outlier_frac=0.01), torch)
+    w_raw = torch.empty((PN, PK // 2), dtype=torch.uint8, device="cuda")
+    s_raw = torch.empty((PN, PK // 32), dtype=torch.uint8, device="cuda")
+    ops.fill_random_u8(w_raw, wl.tensor_seed(3, 3))
+    ops.fill_random_u8(s_raw, wl.tensor_seed(3, 4), 122, 11)
+    wp, sp = ops.repack_weights(w_raw, s_raw)  # load-time derive, not part of a step
+    q = torch.empty((PM, PK), dtype=torch.uint8, device="cuda")
+    qs = torch.empty((PM, PK // 32), dtype=torch.uint8, device="cuda")
+    c = torch.empty((PM, PN), dtype=torch.uint8, device="cuda")
+    d_scale = torch.tensor([1.0 / 64.0], dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i, ev):
+        ops.moe_quant(x, q, qs, PM, K=PK)
+        if ev is not None:
+            ev[0].record(stream)
+        ops.mxfp4_gemm_e4m3(wp, sp, q, qs, c, d_scale, M=PM, m=PN, k=PK)
+        if ev is not None:
+            ev[1].record(stream)
+
+    log(f"config 3: timing {steps} steps after {warmup} warm-up")
+    ms_step, k_avg, k_med, wall = timed_loop(torch, stream, step, None, steps, warmup)
+    flop = 2.0 * PM * PN * PK
+    # quantiser alone, for the record
+    def qstep(i, ev):
+        if ev is not None:
+            ev[0].record(stream)
+        ops.moe_quant(x, q, qs, PM, K=PK)
+        if ev is not None:
+            ev[1].record(stream)
+
+    _, q_avg, _, _ = timed_loop(torch, stream, qstep, None, max(20, steps // 4), 5)
+    q_bytes = PM * PK * 2 + PM * PK + PM * PK // 32
+    return {
+        "ms_per_step": ms_step, "wall_ms_per_step": wall, "flop": flop, "kernel_ms": k_avg, "kernel_ms_median": k_med,
+        "quant_ms": q_avg, "quant_bytes": q_bytes, "tensors": (wp, sp, q, qs),
+    }
+
+
+def bench_decode(torch, ops, wl, stream, steps, warmup, M):
+    wbytes = DN * DK // 2 + DN * DK // 32
+    copies = max(4, -(-2 * MALL_BYTES // wbytes))  # working set > 2x the Infinity Cache
+    log(f"config 2: M={M}, {copies} weight copies of {wbytes / 1e6:.1f} MB")
+    x = dev_from_np(wl.activations_bf16(2, M, DK), torch)
+    ws = []
+    w_raw = torch.empty((DN, DK // 2), dtype=torch.uint8, device="cuda")
+    s_raw = torch.empty((DN, DK // 32), dtype=torch.uint8, device="cuda")
+    for j in range(copies):
+        ops.fill_random_u8(w_raw, wl.tensor_seed(2 + 1000 * j, 3))
+        ops.fill_random_u8(s_raw, wl.tensor_seed(2 + 1000 * j, 4), 122, 11)
+        ws.append(ops.repack_weights(w_raw, s_raw))
+    del w_raw, s_raw
+    y = torch.empty((M, DN), dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i, ev):
+        wp, sp = ws[i % copies]
+        if ev is not None:
+            ev[0].record(stream)
+        ops.mxfp4_gemv_bf16(x, wp, sp, y, M, N=DN, K=DK)
+        if ev is not None:
+            ev[1].record(stream)
+
+    log(f"config 2: timing {steps} launches after {warmup} warm-up")
+    ms_step, k_avg, k_med, wall = timed_loop(torch, stream, step, None, steps, warmup)
+    nbytes = wbytes + 2 * M * DK + 2 * M * DN
+    return {"ms_per_step": ms_step, "kernel_ms": k_avg, "kernel_ms_median": k_med, "bytes": nbytes,
+            "copies": copies, "x": x, "ws": ws}
+
+
+def cpu_baseline_gemm(torch, wl, tensors):
+    """The C oracle on the first rows of the same GEMM (bounded sample), fp32 accumulation."""
+    import numpy as np
+    from oracle import mxoracle as mo
+
+    wp, sp, q, qs = tensors
+    rows = int(os.environ.get("KERN_BENCH_CPU_ROWS", "128"))
+    nt = max(1, min(16, os.cpu_count() or 1))
+    wpn, spn = wp.cpu().numpy(), sp.cpu().numpy()
+    qn, qsn = q[:rows].cpu().numpy(), qs[:rows].cpu().numpy()
+    t = time.perf_counter()
+    mo.gemm_e4m3_pt(wpn, spn, qn, qsn, PN, PK, 1.0 / 64.0, nthreads=nt)
+    dt = time.perf_counter() - t
+    flop = 2.0 * rows * PN * PK
+    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": nt, "kind": "port",
+            "sample": f"config 3 GEMM rows 0..{rows - 1} of {PM} (N={PN}, K={PK}), {dt:.1f} s, "
+                      f"scalar C oracle, {nt} threads over rows"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the MXFP4 path "
+              f"has no sharded mode here", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from kern_amd import ops
+    from kern_amd import workload as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    ops.lib()
+    stream = torch.cuda.Stream()
+    out = {}
+    with torch.cuda.stream(stream):
+        g = d = None
+        if args.only in (None, "gemm"):
+            g = bench_gemm(torch, ops, wl, stream, args.steps, args.warmup)
+        if args.only in (None, "decode"):
+            d = bench_decode(torch, ops, wl, stream, args.steps, args.warmup, args.decode_m)
+    torch.cuda.synchronize()
+
+    cpu = None
+    if g is not None and not args.no_cpu:
+        log("cpu_baseline: timing the C oracle on a sample")
+        cpu = cpu_baseline_gemm(torch, wl, g["tensors"])
+
+    dec = None
+    if d is not None:
+        gbs = d["bytes"] / (d["kernel_ms"] * 1e-3) / 1e9
+        dec = {"metric": f"decode GEMV GB/s M={args.decode_m}", "value": round(gbs, 1), "unit": "GB/s",
+               "ms_per_step": round(d["ms_per_step"], 5),
+               "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                            "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                            "traffic": load_traffic("kern_mx_gemv_bf16"),
+                            "kernel": "kern_mx_gemv_bf16", "kernel_us": round(d["kernel_ms"] * 1e3, 3),
+                            "kernel_us_median": round(d["kernel_ms_median"] * 1e3, 3),
+                            "algorithmic_bytes": d["bytes"]},
+               "config": {"M": args.decode_m, "N": DN, "K": DK, "weight_copies": d["copies"]}}
+
+    if g is not None:
+        value = g["flop"] / (g["ms_per_step"] * 1e-3) / 1e12
+        kt = g["flop"] / (g["kernel_ms"] * 1e-3) / 1e12
+        out = {
+            "metric": "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1",
+            "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(g["ms_per_step"], 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4xmxfp8->f32", "data": "synthetic",
+            "config": {"workload": "config 3 prefill: bf16->MXFP8 quant + MXFP4xMXFP8 GEMM, e4m3 per-tensor out",
+                       "M": PM, "N": PN, "K": PK, "step": "moe_quant + mxfp4_gemm_e4m3"},
+            "roofline": {"bound": "mfma", "achieved": round(kt, 1), "peak": PEAK_MXFP4_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(kt / PEAK_MXFP4_TFLOPS, 4),
+                         "traffic": load_traffic("kern_mx_gemm_e4m3"),
+                         "kernel": "kern_mx_gemm_e4m3", "kernel_us": round(g["kernel_ms"] * 1e3, 3),
+                         "kernel_us_median": round(g["kernel_ms_median"] * 1e3, 3),
+                         "algorithmic_flop": g["flop"],
+                         "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4)},
+            "quantizer": {"kernel": "kern_mx_quant_bf16", "kernel_us": round(g["quant_ms"] * 1e3, 3),
+                          "GB/s": round(g["quant_bytes"] / (g["quant_ms"] * 1e-3) / 1e9, 1),
+                          "algorithmic_bytes": g["quant_bytes"]},
+            "decode": dec,
+            "cpu_baseline": cpu,
+        }
+    else:
+        out = dict(dec)
+        out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+                    "scaling": "weak", "vs_baseline": None, "dtype": "bf16xmxfp4->f32", "data": "synthetic"})
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
