@@ -67,27 +67,32 @@ def dev_from_np(a, torch):
     return torch.from_numpy(a).cuda()
 
 
-def timed_loop(torch, stream, fn_step, kernel_fn, steps, warmup):
-    """Run `warmup` untimed steps, then `steps` timed ones. fn_step(i) enqueues one step; kernel_fn(i)
-    enqueues the dominant kernel of that step, bracketed by events. Returns (ms per step, avg kernel ms)."""
+def timed_loop(torch, stream, fn_step, steps, warmup, per_launch_events=False):
+    """Run `warmup` untimed steps, then `steps` timed ones back to back on `stream`, bracketed by
+    synchronize + HIP events. fn_step(i, ev) enqueues step i; with per_launch_events it also records
+    ev[0]/ev[1] around the step's dominant kernel. Returns (ms per step from the bracketing events,
+    mean and median ms between the per-launch events or None, host wall ms per step)."""
     for i in range(warmup):
         fn_step(i, None)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    evs = None
+    if per_launch_events:
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     t0.record(stream)
     for i in range(steps):
-        fn_step(i, evs[i])
+        fn_step(i, evs[i] if evs else None)
     t1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - w0) * 1e3
-    ms = t0.elapsed_time(t1)
-    kms = [a.elapsed_time(b) for a, b in evs]
-    kms.sort()
-    return ms / steps, sum(kms) / len(kms), kms[len(kms) // 2], wall / steps
+    ms = t0.elapsed_time(t1) / steps
+    if not evs:
+        return ms, None, None, wall / steps
+    kms = sorted(a.elapsed_time(b) for a, b in evs)
+    return ms, sum(kms) / len(kms), kms[len(kms) // 2], wall / steps
 
 
 def load_traffic(kernel):
@@ -118,27 +123,22 @@ def bench_gemm(torch, ops, wl, stream, steps, warmup):
 
     def step(i, ev):
         ops.moe_quant(x, q, qs, PM, K=PK)
-        if ev is not None:
-            ev[0].record(stream)
         ops.mxfp4_gemm_e4m3(wp, sp, q, qs, c, d_scale, M=PM, m=PN, k=PK)
-        if ev is not None:
-            ev[1].record(stream)
+
+    def gemm(i, ev):
+        ops.mxfp4_gemm_e4m3(wp, sp, q, qs, c, d_scale, M=PM, m=PN, k=PK)
+
+    def quant(i, ev):
+        ops.moe_quant(x, q, qs, PM, K=PK)
 
     log(f"config 3: timing {steps} steps after {warmup} warm-up")
-    ms_step, k_avg, k_med, wall = timed_loop(torch, stream, step, None, steps, warmup)
+    ms_step, _, _, wall = timed_loop(torch, stream, step, steps, warmup)
+    k_avg, _, _, _ = timed_loop(torch, stream, gemm, steps, warmup)
+    q_avg, _, _, _ = timed_loop(torch, stream, quant, steps, warmup)
     flop = 2.0 * PM * PN * PK
-    # quantiser alone, for the record
-    def qstep(i, ev):
-        if ev is not None:
-            ev[0].record(stream)
-        ops.moe_quant(x, q, qs, PM, K=PK)
-        if ev is not None:
-            ev[1].record(stream)
-
-    _, q_avg, _, _ = timed_loop(torch, stream, qstep, None, max(20, steps // 4), 5)
     q_bytes = PM * PK * 2 + PM * PK + PM * PK // 32
     return {
-        "ms_per_step": ms_step, "wall_ms_per_step": wall, "flop": flop, "kernel_ms": k_avg, "kernel_ms_median": k_med,
+        "ms_per_step": ms_step, "wall_ms_per_step": wall, "flop": flop, "kernel_ms": k_avg,
         "quant_ms": q_avg, "quant_bytes": q_bytes, "tensors": (wp, sp, q, qs),
     }
 
@@ -161,16 +161,12 @@ def bench_decode(torch, ops, wl, stream, steps, warmup, M):
 
     def step(i, ev):
         wp, sp = ws[i % copies]
-        if ev is not None:
-            ev[0].record(stream)
         ops.mxfp4_gemv_bf16(x, wp, sp, y, M, N=DN, K=DK)
-        if ev is not None:
-            ev[1].record(stream)
 
     log(f"config 2: timing {steps} launches after {warmup} warm-up")
-    ms_step, k_avg, k_med, wall = timed_loop(torch, stream, step, None, steps, warmup)
+    ms_step, _, _, wall = timed_loop(torch, stream, step, steps, warmup)
     nbytes = wbytes + 2 * M * DK + 2 * M * DN
-    return {"ms_per_step": ms_step, "kernel_ms": k_avg, "kernel_ms_median": k_med, "bytes": nbytes,
+    return {"ms_per_step": ms_step, "kernel_ms": ms_step, "bytes": nbytes,
             "copies": copies, "x": x, "ws": ws}
 
 
@@ -180,7 +176,7 @@ def cpu_baseline_gemm(torch, wl, tensors):
     from oracle import mxoracle as mo
 
     wp, sp, q, qs = tensors
-    rows = int(os.environ.get("KERN_BENCH_CPU_ROWS", "128"))
+    rows = int(os.environ.get("KERN_BENCH_CPU_ROWS", str(PM)))
     nt = max(1, min(16, os.cpu_count() or 1))
     wpn, spn = wp.cpu().numpy(), sp.cpu().numpy()
     qn, qsn = q[:rows].cpu().numpy(), qs[:rows].cpu().numpy()
@@ -233,7 +229,6 @@ def main():
                             "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                             "traffic": load_traffic("kern_mx_gemv_bf16"),
                             "kernel": "kern_mx_gemv_bf16", "kernel_us": round(d["kernel_ms"] * 1e3, 3),
-                            "kernel_us_median": round(d["kernel_ms_median"] * 1e3, 3),
                             "algorithmic_bytes": d["bytes"]},
                "config": {"M": args.decode_m, "N": DN, "K": DK, "weight_copies": d["copies"]}}
 
@@ -251,7 +246,6 @@ def main():
                          "frac": round(kt / PEAK_MXFP4_TFLOPS, 4),
                          "traffic": load_traffic("kern_mx_gemm_e4m3"),
                          "kernel": "kern_mx_gemm_e4m3", "kernel_us": round(g["kernel_ms"] * 1e3, 3),
-                         "kernel_us_median": round(g["kernel_ms_median"] * 1e3, 3),
                          "algorithmic_flop": g["flop"],
                          "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4)},
             "quantizer": {"kernel": "kern_mx_quant_bf16", "kernel_us": round(g["quant_ms"] * 1e3, 3),

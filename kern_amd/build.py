@@ -34,7 +34,7 @@ ENTRIES = {
     "kern_mx_w_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
     "kern_mx_sf_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
     "kern_mx_gemv_bf16": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32", "i32",
-                          "i32"],
+                          "i32", "i32", "i32"],
     "kern_mx_bmm_fc2": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
                         "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "i32",
                         "out buffer<f32>"],

@@ -5,6 +5,7 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -274,12 +275,13 @@ struct Args {
   }
 };
 
-int launch(const char* entry, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, void* stream, Args& a) {
+int launch(const char* entry, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, void* stream, Args& a,
+           uint32_t shared_bytes = 0) {
   kern_function f = nullptr;
   if (int rc = function(entry, &f)) return rc;
   if (int rc = kern_function_check_params(f, a.sizes.data(), (int)a.sizes.size())) return rc;
   const uint32_t grid[3] = {gx, gy, gz}, blk[3] = {block, 1, 1};
-  return kern_launch(f, grid, blk, 0, stream, a.buf, (a.n + 7) & ~size_t(7));
+  return kern_launch(f, grid, blk, shared_bytes, stream, a.buf, (a.n + 7) & ~size_t(7));
 }
 
 #define REQUIRE(cond, ...) \
@@ -305,11 +307,12 @@ extern "C" int kern_moe_quant(const void* x, void* q, void* sf, int32_t tokens, 
           tokens);
   if (tokens == 0) return KERN_OK;
   REQUIRE(x && q && sf, "moe_quant: null buffer");
-  const int64_t blocks = (int64_t)tokens * (K / 32);
-  REQUIRE(blocks / 256 < (int64_t)1 << 31, "moe_quant: %lld blocks exceed the grid", (long long)blocks);
+  const int64_t chunks = (int64_t)tokens * (K / 8);  // one lane per 8 elements
+  REQUIRE((chunks + 511) / 512 < (int64_t)1 << 31, "moe_quant: %lld elements exceed the grid",
+          (long long)chunks * 8);
   Args a;
   a.put(x), a.put(q), a.put(sf), a.put(tokens), a.put(K);
-  return launch("kern_mx_quant_bf16", (uint32_t)((blocks + 255) / 256), 1, 1, 256, stream, a);
+  return launch("kern_mx_quant_bf16", (uint32_t)((chunks + 511) / 512), 1, 1, 256, stream, a);
 }
 
 extern "C" int kern_moe_w_shuffle(const void* raw, void* out, int32_t experts, int32_t rows, int32_t row_bytes,
@@ -414,9 +417,26 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
   REQUIRE(M >= 1 && M <= 16 && N > 0 && N % 16 == 0 && K > 0 && K % 512 == 0,
           "mxfp4_gemv_bf16: need 1 <= M <= 16, N %% 16 == 0, K %% 512 == 0 (M=%d N=%d K=%d)", M, N, K);
   REQUIRE(x && w && w_sf && y, "mxfp4_gemv_bf16: null buffer");
+  // sb: k-tiles per wave whose slice of x is staged in LDS at once (at most four 16-byte pieces per lane,
+  // M * sb <= 16, sb divides K/512); nb: k-tiles per wave whose weights are in flight together (the
+  // largest of the kernel's batch sizes dividing sb)
+  const int32_t kq = K / 512;
+  int32_t sb = 1;
+  for (int32_t cand = std::min(kq, 16 / M); cand >= 1; --cand)
+    if (kq % cand == 0) {
+      sb = cand;
+      break;
+    }
+  int32_t nb = 1;
+  for (int32_t cand : {7, 4, 2})
+    if (sb % cand == 0) {
+      nb = cand;
+      break;
+    }
+  const uint32_t lds = (uint32_t)(M + 1) * (uint32_t)(sb * 1024 + 16);  // x slice + one zero row
   Args a;
-  a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K);
-  return launch("kern_mx_gemv_bf16", (uint32_t)(N / 16), 1, 1, 256, stream, a);
+  a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K), a.put(nb), a.put(sb);
+  return launch("kern_mx_gemv_bf16", (uint32_t)(N / 16), 1, 1, 256, stream, a, lds);
 }
 
 extern "C" int kern_fill_random_u8(void* out, int64_t n, uint64_t seed, int32_t lo, int32_t span, void* stream) {

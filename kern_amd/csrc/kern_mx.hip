@@ -20,45 +20,37 @@ struct IC { static constexpr int value = V; };
 
 // ====================================================================================== quantizer
 // op moe_quant (fixtures/k3/head.json:25057): in bf16 x[T][K], out u8 q[T][K], out u8 sf[T][K/32], i32 T,
-// launch i32 K. One thread per 32-element block; grid ceil(T*K/32 / 256), block 256 (the reference grid).
+// launch i32 K. Four lanes per 32-element block, 8 elements (16 bytes) per lane, so every wave-wide
+// load covers 1 KiB of contiguous input and every store 512 contiguous bytes; the block amax is
+// reduced over the lane quad with DPP. Each lane handles chunks i and i + 256 of its workgroup's 512
+// (both loads in flight together). Grid ceil(T*K/8 / 512), block 256.
 extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint16_t* __restrict__ x,
                                                                      uint8_t* __restrict__ q,
                                                                      uint8_t* __restrict__ sf, int T, int K) {
-  const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t nblk = (int64_t)T * (K / 32);
-  if (blk >= nblk) return;
-  const v4u* src = reinterpret_cast<const v4u*>(x + blk * 32);
-  v4u v[4];
+  const int64_t i0 = (int64_t)blockIdx.x * 512 + threadIdx.x;  // 8-element chunk
+  const int64_t n = (int64_t)T * (K >> 3);
+  // a lane quad is in or out of range together (n is a multiple of 4)
+  v4u v[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = __builtin_nontemporal_load(src + i);
-  uint32_t amax = 0;
+  for (int h = 0; h < 2; ++h)
+    if (i0 + 256 * h < n) v[h] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(x) + i0 + 256 * h);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int h = 0; h < 2; ++h) {
+    const int64_t i = i0 + 256 * h;
+    if (i < n) {
+      uint32_t amax = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t w = v[i][j];
-      uint32_t lo = (w << 16) & 0x7fffffffu, hi = w & 0x7fff0000u;
-      amax = max(amax, max(lo, hi));
+      for (int j = 0; j < 4; ++j) amax = max(amax, max((v[h][j] << 16) & 0x7fffffffu, v[h][j] & 0x7fff0000u));
+      amax = max(amax, (uint32_t)__builtin_amdgcn_mov_dpp((int)amax, 0xB1, 0xF, 0xF, false));  // lane ^ 1
+      amax = max(amax, (uint32_t)__builtin_amdgcn_mov_dpp((int)amax, 0x4E, 0xF, 0xF, false));  // lane ^ 2
+      const uint32_t sc = mx_scale_code(amax);
+      uint2 out;
+      out.x = mx_pack4(v[h][0], v[h][1], sc);
+      out.y = mx_pack4(v[h][2], v[h][3], sc);
+      reinterpret_cast<uint2*>(q)[i] = out;
+      if ((threadIdx.x & 3) == 0) sf[i >> 2] = (uint8_t)sc;
     }
-  const uint32_t sc = mx_scale_code(amax);
-  v4u out[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t packed[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint32_t w0 = v[i][2 * h], w1 = v[i][2 * h + 1];
-      uint32_t c0 = mx_elem_code(w0 << 16, sc), c1 = mx_elem_code(w0 & 0xffff0000u, sc);
-      uint32_t c2 = mx_elem_code(w1 << 16, sc), c3 = mx_elem_code(w1 & 0xffff0000u, sc);
-      packed[h] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
-    }
-    out[i / 2][2 * (i % 2)] = packed[0];
-    out[i / 2][2 * (i % 2) + 1] = packed[1];
   }
-  v4u* dst = reinterpret_cast<v4u*>(q + blk * 32);
-  dst[0] = out[0];
-  dst[1] = out[1];
-  sf[blk] = (uint8_t)sc;
 }
 
 // ====================================================================================== repack
@@ -110,53 +102,109 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_sf_shuffle(const uint8
 
 // ====================================================================================== decode GEMV
 // op mxfp4_gemv_bf16 (new; the W4A16 decode of BASELINE configs 1-2): in bf16 x[M][K], in u8 w (repacked,
-// non-gated) [N][K/2], in u8 w_sf (repacked), out bf16 y[M][N], i32 M, launch i32 N, i32 K.
-// Grid N/16, block 256: one 16-row group per workgroup, the four waves split the K groups (512 wide)
-// and reduce through LDS. fp4 is decoded with its scale by V_CVT_SCALEF32_PK_BF16_FP4 and multiplied on
-// V_MFMA_F32_16X16X32_BF16 (tokens are the 16 B columns; columns >= M are zero).
-extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16(const uint16_t* __restrict__ x,
-                                                                    const uint8_t* __restrict__ w,
-                                                                    const uint8_t* __restrict__ wsf,
-                                                                    uint16_t* __restrict__ y, int M, int N, int K) {
+// non-gated) [N][K/2], in u8 w_sf (repacked), out bf16 y[M][N], i32 M, launch i32 N, i32 K, i32 nb.
+// Grid N/16, block 256, dynamic LDS (M+1)*(nb*1024 + 16) bytes: one 16-row group per workgroup. Wave w
+// takes the 128-wide k-tiles kt = 4i + w (equal shares; its scales are byte w of the group's scale
+// dwords). Tiles are consumed in batches of nb per wave (nb divides K/512 and M*nb <= 16). Per batch,
+// every lane first requests its (at most four) 16-byte pieces of the batch's x slice (a contiguous
+// 512*nb-wide k range of every token), then the batch's scales, then its weight fragments, all in
+// straight-line code: memory operations complete in order, so the x pieces are written to LDS while the
+// weights are still in flight and each fragment is multiplied as soon as it lands. At M = 1,
+// K = 7168 one batch covers the row group: each wave has all 14 KiB of its weights in flight at once.
+// fp4 is decoded with its scale by V_CVT_SCALEF32_PK_BF16_FP4 and multiplied on
+// V_MFMA_F32_16X16X32_BF16 (tokens are the 16 B columns; columns >= M are zero); the four partial sums
+// meet in LDS.
+template <int NB>
+KERN_DEV v4f gemv_rows(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr_, __amdgpu_buffer_rsrc_t sr_, uint16_t* xs,
+                       int M, int K, int nk, int sb, int lane, int c, int grp, int wave, bool live) {
+  const int row = sb * 512 + 8;  // LDS row stride in bf16 (16 B pad)
+  const int sshift = 8 * wave;
+  const int per_tok = 64 * sb;
+  const int pieces = M * per_tok;  // <= 1024: at most four per lane
+  // token rows >= M read row M of xs, which holds zeros: the B columns of absent tokens are zero
+  const uint16_t* xl = xs + (live ? c : M) * row + wave * 128 + grp * 32;
+  for (int q = threadIdx.x; q < row / 8; q += 256) reinterpret_cast<v4u*>(xs + M * row)[q] = (v4u){0u, 0u, 0u, 0u};
+  const int wv = (wave * 64 + lane) * 16;  // this lane's byte in a 4 KiB group of four fragments
+  v4f acc[2] = {};  // two chains, so consecutive MFMAs do not wait on each other
+  for (int s0 = 0; s0 < nk; s0 += sb) {
+    // x[:, 512*s0 .. 512*(s0+sb)) in 16-byte pieces q -> token q / per_tok, column (q % per_tok)*8;
+    // lanes past the last piece read beyond the buffer, which returns zeros
+    v4u xv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int q = (int)threadIdx.x + 256 * r;
+      const int t = q / per_tok, col = (q - t * per_tok) * 8;
+      const int off = q < pieces ? (t * K + s0 * 512 + col) * 2 : 0x7ffffff0;
+      xv[r] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+    }
+    for (int i0 = s0; i0 < s0 + sb; i0 += NB) {
+      // scales before weights, so fragment u waits only for itself and the fragments before it; the
+      // scheduling barriers keep the issue order as written
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t sv[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) sv[u] = __builtin_amdgcn_raw_buffer_load_b32(sr_, lane * 4, (i0 + u) * 256, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      v4u wv4[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        wv4[u] = __builtin_amdgcn_raw_buffer_load_b128(wr_, wv, (i0 + u) * 4096, 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (i0 == s0) {
+        if (s0) __syncthreads();  // the previous slice's reads of xs are done
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int q = (int)threadIdx.x + 256 * r;
+          const int t = q / per_tok, col = (q - t * per_tok) * 8;
+          if (q < pieces) *reinterpret_cast<v4u*>(xs + t * row + col) = xv[r];
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const float s = e8m0_to_f32((sv[u] >> sshift) & 0xffu);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // A: 8 fp4 of this lane's row, k = 32*grp + 8*j .. +8 of the tile (dword j of the lane's slot)
+          const uint32_t wd = wv4[u][j];
+          v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
+          v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
+          v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
+          v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
+          v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          const v4u xb = *reinterpret_cast<const v4u*>(xl + (i0 - s0 + u) * 512 + j * 8);
+          acc[j & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, xb), acc[j & 1], 0, 0, 0);
+        }
+      }
+    }
+  }
+  return acc[0] + acc[1];
+}
+
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void kern_mx_gemv_bf16(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,
+    uint16_t* __restrict__ y, int M, int N, int K, int nb, int sb) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M + 1][sb*512 + 8], row M zero
   __shared__ v4f red[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = blockIdx.x;
   const int KT = K >> 7, KG = K >> 9;
-  const int g0 = (KG * wave) >> 2, g1 = (KG * (wave + 1)) >> 2;
+  const int nk = KT >> 2;  // k-tiles of every wave (K % 512 == 0)
   const int c = lane & 15, grp = lane >> 4;
   const bool live = c < M;
-  const v4u* wf = reinterpret_cast<const v4u*>(w + ((int64_t)rg * KT) * 1024) + lane;
-  const uint32_t* sfp = reinterpret_cast<const uint32_t*>(wsf + ((int64_t)rg * KG) * 256) + lane;
-  const uint16_t* xr = x + (int64_t)(live ? c : 0) * K + grp * 32;
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  for (int kg = g0; kg < g1; ++kg) {
-    v4u wv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wv[j] = __builtin_nontemporal_load(wf + (kg * 4 + j) * 64);
-    const uint32_t sdw = sfp[kg * 64];
-    v4u xv[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const v4u* xp = reinterpret_cast<const v4u*>(xr + (kg * 4 + j) * 128);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[j][i] = live ? xp[i] : (v4u){0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float s = e8m0_to_f32((sdw >> (8 * j)) & 0xffu);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // A: 8 fp4 of this lane's row, k = 32*grp + 8*i .. +8 (dword i of the fragment slot)
-        const uint32_t wd = wv[j][i];
-        v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
-        v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
-        v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
-        v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
-        v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-        v8bf b = __builtin_bit_cast(v8bf, xv[j][i]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-      }
-    }
+  // buffer resources: this row group's fragments and scales, and x (out-of-range reads return zero)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr_ =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(w + (int64_t)rg * KT * 1024), (short)0, KT * 1024, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr_ =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wsf + (int64_t)rg * KG * 256), (short)0, KG * 256, 0x00020000);
+  v4f acc;
+  switch (nb) {
+    case 7: acc = gemv_rows<7>(xr, wr_, sr_, xs, M, K, nk, sb, lane, c, grp, wave, live); break;
+    case 4: acc = gemv_rows<4>(xr, wr_, sr_, xs, M, K, nk, sb, lane, c, grp, wave, live); break;
+    case 2: acc = gemv_rows<2>(xr, wr_, sr_, xs, M, K, nk, sb, lane, c, grp, wave, live); break;
+    default: acc = gemv_rows<1>(xr, wr_, sr_, xs, M, K, nk, sb, lane, c, grp, wave, live); break;
   }
   red[wave][lane] = acc;
   __syncthreads();
