@@ -282,10 +282,12 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int m = A.m;
 
-  uint8_t* ldsW[2] = {lds, lds + LDS_W};
-  uint8_t* ldsX[2] = {lds + 2 * LDS_W, lds + 2 * LDS_W + LDS_X};
-  uint8_t* ldsSW[2] = {lds + 2 * (LDS_W + LDS_X), lds + 2 * (LDS_W + LDS_X) + LDS_SW};
-  uint8_t* ldsSX[2] = {lds + 2 * (LDS_W + LDS_X + LDS_SW), lds + 2 * (LDS_W + LDS_X + LDS_SW) + LDS_SX};
+  // LDS regions as byte offsets from `lds` (integer offsets keep every access a ds_* instruction; a
+  // pointer picked from an array at run time would degrade to a flat access)
+  auto ldsW = [&](int b) { return lds + b * LDS_W; };
+  auto ldsX = [&](int b) { return lds + 2 * LDS_W + b * LDS_X; };
+  auto ldsSW = [&](int b) { return lds + 2 * (LDS_W + LDS_X) + b * LDS_SW; };
+  auto ldsSX = [&](int b) { return lds + 2 * (LDS_W + LDS_X + LDS_SW) + b * LDS_SX; };
 
   // global sources
   const int rg0 = (nx * BN) >> 4;  // first 16-row group of this tile
@@ -313,25 +315,27 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
     srow = sok ? r : 0;
   }
 
-  v4u gw[4], gx4[4];
+  // Two register stages: tile kt+2 is requested at the start of step kt, tile kt+1 (requested a step
+  // earlier) is written to LDS at its end, so every global load has two steps of MFMA work to land.
+  v4u gw[2][4], gx4[2][4];
   v4u gsw;
   uint32_t gsx[2];
 
-  auto load_tile = [&](int kt) {
+  auto load_tile = [&](int kt, int r) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int f = i * 4 + (tid >> 6);  // fragment (row group) 0..15
-      gw[i] = *(reinterpret_cast<const v4u*>(wbase + ((int64_t)f * KT + kt) * 1024) + lane);
+      gw[r][i] = *(reinterpret_cast<const v4u*>(wbase + ((int64_t)f * KT + kt) * 1024) + lane);
     }
+    // rows past the slot's last valid row load row 0 / token 0 instead (unconditional loads keep the
+    // wait counts exact; their accumulators are never stored)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (xok[i])
-        gx4[i] = *reinterpret_cast<const v4u*>(A.b + xrow[i] * K + (int64_t)kt * 128 + xj * 16);
-    }
+    for (int i = 0; i < 4; ++i)
+      gx4[r][i] = *reinterpret_cast<const v4u*>(A.b + xrow[i] * K + (int64_t)kt * 128 + xj * 16);
   };
   auto load_scales = [&](int kg) {
     gsw = *reinterpret_cast<const v4u*>(sbase + ((int64_t)(tid >> 4) * KG + kg) * 256 + (tid & 15) * 16);
-    if (sok) {
+    {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kt = kg * 4 + sq * 2 + h;
@@ -346,24 +350,22 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
       }
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, int r) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int f = i * 4 + (tid >> 6);
-      *reinterpret_cast<v4u*>(ldsW[buf] + f * 1024 + lane * 16) = gw[i];
+      *reinterpret_cast<v4u*>(ldsW(buf) + f * 1024 + lane * 16) = gw[r][i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = (tid >> 3) + 32 * i;
-      if (xok[i]) *reinterpret_cast<v4u*>(ldsX[buf] + t * 128 + ((xj ^ ((t >> 1) & 7)) << 4)) = gx4[i];
+      *reinterpret_cast<v4u*>(ldsX(buf) + t * 128 + ((xj ^ ((t >> 1) & 7)) << 4)) = gx4[r][i];
     }
   };
   auto store_scales = [&](int buf) {
-    *reinterpret_cast<v4u*>(ldsSW[buf] + tid * 16) = gsw;
-    if (sok) {
+    *reinterpret_cast<v4u*>(ldsSW(buf) + tid * 16) = gsw;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) reinterpret_cast<uint32_t*>(ldsSX[buf])[(sq * 2 + h) * BT + st] = gsx[h];
-    }
+    for (int h = 0; h < 2; ++h) reinterpret_cast<uint32_t*>(ldsSX(buf))[(sq * 2 + h) * BT + st] = gsx[h];
   };
 
   v4f acc[4][8];
@@ -377,37 +379,40 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
   const int c = lane & 15, g = lane >> 4;
 
   load_scales(0);
-  load_tile(0);
+  load_tile(0, 0);
+  if (KT > 1) load_tile(1, 1);
   store_scales(0);
-  store_tile(0);
+  store_tile(0, 0);
   __syncthreads();
 
+  uint32_t swd[8];  // this wave's weight-scale dwords of the current 512-wide k group
   auto step = [&](int kg, auto Jc) {
     constexpr int j = decltype(Jc)::value;
+    constexpr int r = j & 1;  // register stage of tile kt (kt = 4*kg + j has the parity of j)
     const int sb = kg & 1;
     const int kt = kg * 4 + j;
     const int buf = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) load_tile(kt + 1);
-    if (j == 3 && more) load_scales(kg + 1);
-    uint32_t swd[8];
+    if (kt + 2 < KT) load_tile(kt + 2, r);           // tile kt left stage r for LDS a step ago
+    if (j == 2 && kg + 1 < KG) load_scales(kg + 1);  // written to LDS at the end of step 4*kg + 3
+    if (j == 0) {
 #pragma unroll
-    for (int rs = 0; rs < 8; ++rs)
-      swd[rs] = reinterpret_cast<const uint32_t*>(ldsSW[sb] + (wn * 8 + rs) * 256)[lane];
+      for (int rs = 0; rs < 8; ++rs)
+        swd[rs] = reinterpret_cast<const uint32_t*>(ldsSW(sb) + (wn * 8 + rs) * 256)[lane];
+    }
     v4i wa[8];
 #pragma unroll
     for (int rs = 0; rs < 8; ++rs)
-      wa[rs] = *reinterpret_cast<const v4i*>(ldsW[buf] + (wn * 8 + rs) * 1024 + lane * 16);
+      wa[rs] = *reinterpret_cast<const v4i*>(ldsW(buf) + (wn * 8 + rs) * 1024 + lane * 16);
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       if (ts < live_ts) {
         const int t = wt * 64 + ts * 16 + c;
-        const uint8_t* xr = ldsX[buf] + t * 128;
+        const uint8_t* xr = ldsX(buf) + t * 128;
         const int sw = (t >> 1) & 7;
         v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
         v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
         v8i xb = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        const uint32_t sx = reinterpret_cast<const uint32_t*>(ldsSX[sb])[j * BT + t] >> (8 * g);
+        const uint32_t sx = reinterpret_cast<const uint32_t*>(ldsSX(sb))[j * BT + t] >> (8 * g);
 #pragma unroll
         for (int rs = 0; rs < 8; ++rs) {
           v8i wb = {wa[rs][0], wa[rs][1], wa[rs][2], wa[rs][3], 0, 0, 0, 0};
@@ -416,9 +421,9 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
         }
       }
     }
-    if (more) {
+    if (kt + 1 < KT) {
       if (j == 3) store_scales(sb ^ 1);
-      store_tile(buf ^ 1);
+      store_tile(buf ^ 1, r ^ 1);
     }
     __syncthreads();
   };
@@ -462,9 +467,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
           const int n = wrow0 + rs * 16 + g * 4;
           const v4f v = acc[ts][rs];
           if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
-          uint32_t o = 0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o |= e4m3_rne(__float_as_uint(v[i] * ds), 0) << (8 * i);
+          const uint32_t o = e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
           *reinterpret_cast<uint32_t*>(C + p * m + n) = o;
         }
       }
@@ -517,8 +520,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
 #pragma unroll
           for (int rs = 0; rs < 4; ++rs) {
             const int n = ncol0 + 8 * (bk * 4 + rs) + 2 * g;
-            uint32_t o = mx_elem_code(__float_as_uint(h[bk * 4 + rs][0]), sc) |
-                         (mx_elem_code(__float_as_uint(h[bk * 4 + rs][1]), sc) << 8);
+            const uint32_t o = mx_code2(h[bk * 4 + rs][0], h[bk * 4 + rs][1], sc);
             *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
           }
           if (g == 0) {

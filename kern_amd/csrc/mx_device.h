@@ -130,6 +130,15 @@ KERN_DEV uint32_t mx_pack4(uint32_t w0, uint32_t w1, uint32_t sc) {
   return (uint32_t)r;
 }
 
+// two MXFP8 element codes (low byte = a) of f32 values in a block with scale code sc: e4m3(v * 2^(127-sc))
+// through the hardware converter, or 0x7f|sign when the block is non-finite (sc == 255)
+KERN_DEV uint32_t mx_code2(float a, float b, uint32_t sc) {
+  if (sc == 255u)
+    return (((__float_as_uint(a) >> 24) & 0x80u) | 0x7fu) | ((((__float_as_uint(b) >> 24) & 0x80u) | 0x7fu) << 8);
+  const int sh = 127 - (int)sc;
+  return e4m3_hw2(__builtin_ldexpf(a, sh), __builtin_ldexpf(b, sh));
+}
+
 // f32 value 2^(code-127) (code 0 is the subnormal 2^-127, 255 is NaN)
 KERN_DEV float e8m0_to_f32(uint32_t code) {
   const uint32_t b = code == 0u ? 0x00400000u : (code == 255u ? 0x7fc00000u : code << 23);  // selects, no branches
