@@ -224,11 +224,13 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 // ====================================================================================== block-scaled GEMM
 // One workgroup computes a 128-row (token/slot) x 256-row (weight) tile with 4 waves in a 2x2 grid; each
 // wave owns 64 x 128 = 4 x 8 tiles of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (A = fp4 weights, B = e4m3
-// activations, e8m0 scales in-instruction). K advances 128 per step through double-buffered LDS:
-//   W: 16 fragments of 1 KiB, copied verbatim (the repacked layout is the MFMA operand layout);
-//   X: 128 rows x 128 B, 16-byte chunk j of row t stored at t*128 + ((j ^ ((t>>1)&7)) << 4) so that both
-//      the row-wise writes and the fragment reads (rows 0..15, one chunk) touch 16 distinct bank groups;
-//   scales once per 512 of K: W fragments verbatim, X as dwords [k-tile][row].
+// activations, e8m0 scales in-instruction). K advances in 128-wide k-tiles through a four-stage LDS ring
+// filled by direct global->LDS loads (GLOBAL_LOAD_LDS_DWORDX4), three tiles ahead of the MFMAs:
+//   W stage: 16 fragments of 1 KiB, copied verbatim (the repacked layout is the MFMA operand layout);
+//   X stage: 128 rows x 128 B, 16-byte chunk j of row t stored at t*128 + ((j ^ ((t>>1)&7)) << 4) so that
+//      the fragment reads (16 rows, one chunk each) touch distinct bank groups; the permutation is
+//      applied on the global side, each lane fetching the chunk that belongs at its LDS position;
+//   scales once per 512 of K (two slots): W fragments verbatim, X as dwords [k-tile][row].
 enum { MODE_FC2 = 0, MODE_FC1 = 1, MODE_PT = 2, MODE_DENSE_BF16 = 3 };
 
 struct BmmArgs {
@@ -257,9 +259,35 @@ struct BmmArgs {
 #define LDS_SW (16 * 256)
 #define LDS_SX (4 * BT * 4)
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glob_void_t;
+
+// 16 bytes per lane from global memory straight into LDS at `lds_wave_base + 16 * lane` (wave-uniform base)
+KERN_DEV void dma16(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glob_void_t*)g, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+// 4 bytes per lane, to `lds_wave_base + 4 * lane`
+KERN_DEV void dma4(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glob_void_t*)g, (lds_void_t*)lds_wave_base, 4, 0, 0);
+}
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+// lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | 0x70 | 0xF00 | (((n) >> 4) << 14))
+
+// The LDS ring. Each stage and scale slot is its own variable, so that the compiler's wait-count
+// analysis can tell a read of one stage from the loads still landing in another.
+struct BmmLds {
+  uint8_t* w[4];
+  uint8_t* x[4];
+  uint8_t* sw[2];
+  uint8_t* sx[2];
+};
+
 template <int MODE>
-KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
+  // the wave index through readfirstlane: provably uniform, so everything derived from it (the LDS
+  // bases of the direct loads) lives in scalar registers
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wt = wave >> 1, wn = wave & 1;
   const int gx = A.m / BN;
   // XCD-aware linearisation: consecutive workgroups land on different XCDs (round robin over 8); give
@@ -282,90 +310,54 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int m = A.m;
 
-  // LDS regions as byte offsets from `lds` (integer offsets keep every access a ds_* instruction; a
-  // pointer picked from an array at run time would degrade to a flat access)
-  auto ldsW = [&](int b) { return lds + b * LDS_W; };
-  auto ldsX = [&](int b) { return lds + 2 * LDS_W + b * LDS_X; };
-  auto ldsSW = [&](int b) { return lds + 2 * (LDS_W + LDS_X) + b * LDS_SW; };
-  auto ldsSX = [&](int b) { return lds + 2 * (LDS_W + LDS_X + LDS_SW) + b * LDS_SX; };
-
   // global sources
   const int rg0 = (nx * BN) >> 4;  // first 16-row group of this tile
   const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)rg0 * KT) * 1024;
   const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)rg0 * KG) * 256;
-  // X rows this thread stages: t = tid/8 + 32*i (i = 0..3), chunk j = tid%8
-  const int xj = tid & 7;
-  int64_t xrow[4];
-  bool xok[4];
+  // token (activation row) of tile row t; rows past the slot's last valid row read row/token 0
+  // (their accumulators are never stored)
+  auto token_of = [&](int t) -> int64_t {
+    if (t >= valid) return 0;
+    if (MODE == MODE_FC1) return A.route_map[row0 + t];
+    return row0 + t;
+  };
+  // X tile DMA: instruction r of this wave fills LDS rows 32r + 8*wave + lane/8, position lane%8
+  const int xpos = lane & 7;
+  const uint8_t* xsrc[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = (tid >> 3) + 32 * i;
-    xok[i] = t < valid;
-    int64_t r = row0 + t;
-    if (MODE == MODE_FC1) r = xok[i] ? A.route_map[row0 + t] : 0;
-    xrow[i] = xok[i] ? r : 0;
+  for (int r = 0; r < 4; ++r) {
+    const int t = 32 * r + 8 * wave + (lane >> 3);
+    xsrc[r] = A.b + token_of(t) * K + ((xpos ^ ((t >> 1) & 7)) << 4);
   }
-  // X scale staging: thread -> (row t = tid & 127, k-tile pair q = tid >> 7): two dwords each
-  const int st = tid & 127, sq = tid >> 7;
-  int64_t srow;
-  bool sok = st < valid;
-  {
-    int64_t r = row0 + st;
-    if (MODE == MODE_FC1) r = sok ? A.route_map[row0 + st] : 0;
-    srow = sok ? r : 0;
-  }
+  // X scale DMA (dwords): this lane's row (64*wave + lane) & 127; instruction r covers k-tile 2r + wave/2
+  const int64_t srow = token_of((64 * wave + lane) & 127);
+  auto sx_src = [&](int kg, int r) -> const uint8_t* {
+    const int kt = kg * 4 + 2 * r + (wave >> 1);
+    if (A.sf_b_r128c4) {
+      const int64_t kb4 = K >> 7;  // ceil(kblocks/4) with K % 128 == 0
+      return A.sf_b + 512 * ((srow >> 7) * kb4 + kt) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
+    }
+    return A.sf_b + srow * (K >> 5) + kt * 4;
+  };
 
-  // Two register stages: tile kt+2 is requested at the start of step kt, tile kt+1 (requested a step
-  // earlier) is written to LDS at its end, so every global load has two steps of MFMA work to land.
-  v4u gw[2][4], gx4[2][4];
-  v4u gsw;
-  uint32_t gsx[2];
-
-  auto load_tile = [&](int kt, int r) {
+  // requests of one tile (8 per wave) and of one k group's scales (3 per wave); indices past the end are
+  // clamped to the last tile / group, whose data is then never multiplied
+  auto dma_tile = [&](int kt, uint8_t* sW, uint8_t* sX) {
+    kt = min(kt, KT - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = i * 4 + (tid >> 6);  // fragment (row group) 0..15
-      gw[r][i] = *(reinterpret_cast<const v4u*>(wbase + ((int64_t)f * KT + kt) * 1024) + lane);
+    for (int r = 0; r < 4; ++r) {
+      const int f = r * 4 + wave;  // fragment (row group) 0..15
+      dma16(wbase + ((int64_t)f * KT + kt) * 1024 + lane * 16, sW + f * 1024);
     }
-    // rows past the slot's last valid row load row 0 / token 0 instead (unconditional loads keep the
-    // wait counts exact; their accumulators are never stored)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      gx4[r][i] = *reinterpret_cast<const v4u*>(A.b + xrow[i] * K + (int64_t)kt * 128 + xj * 16);
+    for (int r = 0; r < 4; ++r) dma16(xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + wave) * 1024);
   };
-  auto load_scales = [&](int kg) {
-    gsw = *reinterpret_cast<const v4u*>(sbase + ((int64_t)(tid >> 4) * KG + kg) * 256 + (tid & 15) * 16);
-    {
+  auto dma_scales = [&](int kg, uint8_t* sSW, uint8_t* sSX) {
+    kg = min(kg, KG - 1);
+    const int f = 4 * wave + (lane >> 4);
+    dma16(sbase + ((int64_t)f * KG + kg) * 256 + (lane & 15) * 16, sSW + 1024 * wave);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int kt = kg * 4 + sq * 2 + h;
-        int64_t off;
-        if (A.sf_b_r128c4) {
-          const int64_t kb4 = K >> 7;  // ceil(kblocks/4) with K % 128 == 0
-          off = 512 * ((srow >> 7) * kb4 + kt) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
-        } else {
-          off = srow * (K >> 5) + kt * 4;
-        }
-        gsx[h] = *reinterpret_cast<const uint32_t*>(A.sf_b + off);
-      }
-    }
-  };
-  auto store_tile = [&](int buf, int r) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = i * 4 + (tid >> 6);
-      *reinterpret_cast<v4u*>(ldsW(buf) + f * 1024 + lane * 16) = gw[r][i];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = (tid >> 3) + 32 * i;
-      *reinterpret_cast<v4u*>(ldsX(buf) + t * 128 + ((xj ^ ((t >> 1) & 7)) << 4)) = gx4[r][i];
-    }
-  };
-  auto store_scales = [&](int buf) {
-    *reinterpret_cast<v4u*>(ldsSW(buf) + tid * 16) = gsw;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) reinterpret_cast<uint32_t*>(ldsSX(buf))[(sq * 2 + h) * BT + st] = gsx[h];
+    for (int r = 0; r < 2; ++r) dma4(sx_src(kg, r), sSX + 4 * (r * 4 + wave) * 64);
   };
 
   v4f acc[4][8];
@@ -378,61 +370,118 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
   const int live_ts = min(4, max(0, (valid - wt * 64 + 15) >> 4));
   const int c = lane & 15, g = lane >> 4;
 
-  load_scales(0);
-  load_tile(0, 0);
-  if (KT > 1) load_tile(1, 1);
-  store_scales(0);
-  store_tile(0, 0);
-  __syncthreads();
+  // prologue: scales of group 0, tiles 0..2 in flight; wait for the scales and tile 0
+  dma_scales(0, L.sw[0], L.sx[0]);
+  dma_tile(0, L.w[0], L.x[0]);
+  dma_tile(1, L.w[1], L.x[1]);
+  dma_tile(2, L.w[2], L.x[2]);
+  WAIT_VMCNT(16);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
-  uint32_t swd[8];  // this wave's weight-scale dwords of the current 512-wide k group
-  auto step = [&](int kg, auto Jc) {
-    constexpr int j = decltype(Jc)::value;
-    constexpr int r = j & 1;  // register stage of tile kt (kt = 4*kg + j has the parity of j)
-    const int sb = kg & 1;
-    const int kt = kg * 4 + j;
-    const int buf = kt & 1;
-    if (kt + 2 < KT) load_tile(kt + 2, r);           // tile kt left stage r for LDS a step ago
-    if (j == 2 && kg + 1 < KG) load_scales(kg + 1);  // written to LDS at the end of step 4*kg + 3
-    if (j == 0) {
+  auto run = [&](auto NTSc) {
+    constexpr int NTS = decltype(NTSc)::value;  // live token subtiles of this wave (uniform)
+    v4i wa[2][8];       // W operands of tile kt (set kt&1) and kt+1
+    v8i xbuf[2];        // X operand of the current and the next subtile
+    uint32_t sxv[2];    // X scale dwords of the same
+    uint32_t swd[8], swn[8];  // weight-scale dwords of the current and the next k group
+    auto read_w = [&](const uint8_t* sW, int set) {
 #pragma unroll
-      for (int rs = 0; rs < 8; ++rs)
-        swd[rs] = reinterpret_cast<const uint32_t*>(ldsSW(sb) + (wn * 8 + rs) * 256)[lane];
-    }
-    v4i wa[8];
+      for (int rs = 0; rs < 8; ++rs) wa[set][rs] = *reinterpret_cast<const v4i*>(sW + (wn * 8 + rs) * 1024 + lane * 16);
+    };
+    auto read_x = [&](const uint8_t* sX, const uint8_t* sSX, int jt, int ts, int xs) {
+      const int t = wt * 64 + ts * 16 + c;
+      const uint8_t* xr = sX + t * 128;
+      const int sw = (t >> 1) & 7;
+      const v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
+      const v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
+      xbuf[xs] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      sxv[xs] = reinterpret_cast<const uint32_t*>(sSX)[jt * BT + t] >> (8 * g);
+    };
+    auto read_sw = [&](const uint8_t* sSW, uint32_t* dst) {
 #pragma unroll
-    for (int rs = 0; rs < 8; ++rs)
-      wa[rs] = *reinterpret_cast<const v4i*>(ldsW(buf) + (wn * 8 + rs) * 1024 + lane * 16);
+      for (int rs = 0; rs < 8; ++rs) dst[rs] = reinterpret_cast<const uint32_t*>(sSW + (wn * 8 + rs) * 256)[lane];
+    };
+    auto mfmas = [&](int set, int ts, int xs, auto Jt) {
+      constexpr int jt = decltype(Jt)::value;  // k-tile within the group: scale byte of the weights
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      if (ts < live_ts) {
-        const int t = wt * 64 + ts * 16 + c;
-        const uint8_t* xr = ldsX(buf) + t * 128;
-        const int sw = (t >> 1) & 7;
-        v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
-        v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
-        v8i xb = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        const uint32_t sx = reinterpret_cast<const uint32_t*>(ldsSX(sb))[j * BT + t] >> (8 * g);
-#pragma unroll
-        for (int rs = 0; rs < 8; ++rs) {
-          v8i wb = {wa[rs][0], wa[rs][1], wa[rs][2], wa[rs][3], 0, 0, 0, 0};
-          acc[ts][rs] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb, acc[ts][rs], 4, 0, j,
-                                                                          (int)swd[rs], 0, (int)sx);
-        }
+      for (int rs = 0; rs < 8; ++rs) {
+        const v8i wb = {wa[set][rs][0], wa[set][rs][1], wa[set][rs][2], wa[set][rs][3], 0, 0, 0, 0};
+        acc[ts][rs] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xbuf[xs], acc[ts][rs], 4, 0, jt,
+                                                                        (int)swd[rs], 0, (int)sxv[xs]);
       }
+    };
+
+    read_sw(L.sw[0], swd);
+    read_w(L.w[0], 0);
+    if (NTS > 0) read_x(L.x[0], L.sx[0], 0, 0, 0);
+
+    // step J of a pair of k groups: tile kt = 8*kk + J, stage kt % 4 = J % 4, scale slot = J / 4
+    auto step = [&](int kk, auto Jc) {
+      constexpr int J = decltype(Jc)::value;
+      constexpr int jt = J & 3, st = J & 3, sb = J >> 2;
+      constexpr int cur = J & 1, nxt = cur ^ 1;
+      constexpr int st1 = (st + 1) & 3, st3 = (st + 3) & 3;
+      constexpr int sb1 = jt == 3 ? sb ^ 1 : sb;  // scale slot of tile kt+1
+      const int kt = kk * 8 + J;
+      const int kg = kt >> 2;
+      // phase 0: requests for later tiles (the stage of tile kt+3 was last read before the previous
+      // barrier), then the first subtile
+      if (jt == 0) dma_scales(kg + 1, L.sw[sb ^ 1], L.sx[sb ^ 1]);
+      dma_tile(kt + 3, L.w[st3], L.x[st3]);
+      if (NTS > 1) read_x(L.x[st], L.sx[sb], jt, 1, 1);
+      if (NTS > 0) mfmas(cur, 0, 0, IC<jt>{});
+      __builtin_amdgcn_sched_barrier(0);
+      // phases 1, 2
+      if (NTS > 2) read_x(L.x[st], L.sx[sb], jt, 2, 0);
+      if (NTS > 1) mfmas(cur, 1, 1, IC<jt>{});
+      __builtin_amdgcn_sched_barrier(0);
+      if (NTS > 3) read_x(L.x[st], L.sx[sb], jt, 3, 1);
+      if (NTS > 2) mfmas(cur, 2, 0, IC<jt>{});
+      __builtin_amdgcn_sched_barrier(0);
+      // tile kt+1 (requested in step kt-2) has landed for this wave once at most the requests issued
+      // after it are outstanding: tiles kt+2, kt+3 (8 each) and the scales requested in steps kt-1, kt
+      WAIT_VMCNT(16 + (jt == 1 ? 3 : 0) + (jt == 0 ? 3 : 0));
+      __builtin_amdgcn_s_barrier();  // ... and for every wave; every read of stage kt%4's subtiles 1-3 is issued
+      __builtin_amdgcn_sched_barrier(0);
+      // phase 3: operands of tile kt+1 (the first tile of group kg+1 when jt == 3)
+      read_w(L.w[st1], nxt);
+      if (jt == 3) read_sw(L.sw[sb1], swn);
+      if (NTS > 0) read_x(L.x[st1], L.sx[sb1], (jt + 1) & 3, 0, 0);
+      if (NTS > 3) mfmas(cur, 3, 1, IC<jt>{});
+      if (jt == 3) {
+#pragma unroll
+        for (int rs = 0; rs < 8; ++rs) swd[rs] = swn[rs];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    const int pairs = KG >> 1;
+    for (int kk = 0; kk < pairs; ++kk) {
+      step(kk, IC<0>{});
+      step(kk, IC<1>{});
+      step(kk, IC<2>{});
+      step(kk, IC<3>{});
+      step(kk, IC<4>{});
+      step(kk, IC<5>{});
+      step(kk, IC<6>{});
+      step(kk, IC<7>{});
     }
-    if (kt + 1 < KT) {
-      if (j == 3) store_scales(sb ^ 1);
-      store_tile(buf ^ 1, r ^ 1);
+    if (KG & 1) {  // last (even-numbered) group
+      step(pairs, IC<0>{});
+      step(pairs, IC<1>{});
+      step(pairs, IC<2>{});
+      step(pairs, IC<3>{});
     }
-    __syncthreads();
   };
-  for (int kg = 0; kg < KG; ++kg) {
-    step(kg, IC<0>{});
-    step(kg, IC<1>{});
-    step(kg, IC<2>{});
-    step(kg, IC<3>{});
+  switch (live_ts) {
+    case 4: run(IC<4>{}); break;
+    case 3: run(IC<3>{}); break;
+    case 2: run(IC<2>{}); break;
+    case 1: run(IC<1>{}); break;
+    default: run(IC<0>{}); break;
   }
+  // the ring's last requests (clamped re-reads) must land before the workgroup's LDS is released
+  WAIT_VMCNT(0);
 
   // ---- epilogue: lane (c, g) of tile (ts, rs) holds weight rows 16*rs + 4*g + i, token row c
   const int wrow0 = nx * BN + wn * 128;  // first weight row of this wave
@@ -535,7 +584,12 @@ KERN_DEV void bmm_tile(const BmmArgs& A, uint8_t* lds) {
   }
 }
 
-#define BMM_LDS_BYTES (2 * (LDS_W + LDS_X + LDS_SW + LDS_SX))
+// the LDS ring of one GEMM workgroup: 4 x (16 + 16) KiB tile stages + 2 x (4 + 2) KiB scale slots = 140 KiB
+#define BMM_LDS_DECL(L)                                                                                  \
+  __shared__ __attribute__((aligned(1024))) uint8_t w0_[LDS_W], w1_[LDS_W], w2_[LDS_W], w3_[LDS_W];          \
+  __shared__ __attribute__((aligned(1024))) uint8_t x0_[LDS_X], x1_[LDS_X], x2_[LDS_X], x3_[LDS_X];          \
+  __shared__ __attribute__((aligned(1024))) uint8_t sw0_[LDS_SW], sw1_[LDS_SW], sx0_[LDS_SX], sx1_[LDS_SX]; \
+  const BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}}
 
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
 // a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
@@ -545,13 +599,13 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
     const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
     int sf_b_r128c4, float* dbg) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
   (void)total_padded;
-  bmm_tile<MODE_FC2>(A, lds);
+  bmm_tile<MODE_FC2>(A, L);
 }
 
 // op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
@@ -561,14 +615,14 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc1(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
     const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
     const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, float* dbg) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.sf_c = sf_c; A.route_map = route_map;
   A.alpha = alpha; A.beta = beta;
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
   (void)total_padded;
-  bmm_tile<MODE_FC1>(A, lds);
+  bmm_tile<MODE_FC1>(A, L);
 }
 
 // Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).
@@ -578,22 +632,22 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_e4m3(const uint8_
                                                                     const uint8_t* b, const uint8_t* sf_b,
                                                                     uint8_t* c, const float* d_scale, int M, int m,
                                                                     int k, float* dbg) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.d_scale = d_scale;
   A.m = m; A.k = k; A.rows = M; A.sf_b_r128c4 = 0; A.dbg = dbg;
-  bmm_tile<MODE_PT>(A, lds);
+  bmm_tile<MODE_PT>(A, L);
 }
 
 // Dense bf16-output mode of the FC2 family (one batch, no routing tables).
 extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_bf16(const uint8_t* a, const uint8_t* sf_a,
                                                                     const uint8_t* b, const uint8_t* sf_b,
                                                                     uint16_t* c, int M, int m, int k, float* dbg) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[BMM_LDS_BYTES];
+  BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
   A.m = m; A.k = k; A.rows = M; A.sf_b_r128c4 = 0; A.dbg = dbg;
-  bmm_tile<MODE_DENSE_BF16>(A, lds);
+  bmm_tile<MODE_DENSE_BF16>(A, L);
 }
 
 // ====================================================================================== routing
