@@ -11,6 +11,9 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
 * `roofline` = the GEMM kernel alone: algorithmic FLOPs per launch / its average launch time, measured
   with HIP events on the stream it runs on, against the dense MXFP4 MFMA peak (10.1 PFLOP/s); the
   fraction against the FP8 MFMA rate (5.0 PFLOP/s, the rate of an fp8-operand scaled MFMA) is given too.
+* Every timed loop is captured once into a HIP graph and replayed, so host launch overhead (Python,
+  ctypes, a profiler's API hooks) cannot starve the GPU; back-to-back dispatches then leave no gap, and
+  the per-launch averages agree with rocprofv3's per-dispatch durations.
 * `decode` = config 2 at M=1: W4A16 GEMV over [18432, 7168] MXFP4 weights, rotating over enough weight
   copies (> 256 MB, the Infinity Cache) that every launch streams its weights from HBM; GB/s of
   algorithmic bytes against the 8 TB/s HBM peak.
@@ -48,8 +51,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["gemm", "decode"], default=None,
-                    help="run one leg only (for profiling); the JSON line then carries that leg")
+    ap.add_argument("--only", choices=["gemm", "decode", "copy"], default=None,
+                    help="run one leg only (for profiling); the JSON line then carries that leg. 'copy' runs "
+                         "three plain 256 MiB device copies: the reference for scaling HBM byte counters")
     ap.add_argument("--decode-m", type=int, default=1)
     return ap.parse_args()
 
@@ -67,32 +71,39 @@ def dev_from_np(a, torch):
     return torch.from_numpy(a).cuda()
 
 
-def timed_loop(torch, stream, fn_step, steps, warmup, per_launch_events=False):
-    """Run `warmup` untimed steps, then `steps` timed ones back to back on `stream`, bracketed by
-    synchronize + HIP events. fn_step(i, ev) enqueues step i; with per_launch_events it also records
-    ev[0]/ev[1] around the step's dominant kernel. Returns (ms per step from the bracketing events,
-    mean and median ms between the per-launch events or None, host wall ms per step)."""
-    for i in range(warmup):
-        fn_step(i, None)
-    torch.cuda.synchronize()
-    evs = None
-    if per_launch_events:
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+def timed_loop(torch, stream, fn_step, steps, warmup, graph=True):
+    """Time `steps` back-to-back steps on `stream`. fn_step(i) enqueues step i. With `graph` the steps
+    are captured once into a HIP graph and the graph is replayed, so host-side launch overhead (Python,
+    ctypes, a profiler's API hooks) cannot starve the GPU; the timed region is bracketed by
+    synchronize + HIP events on the stream. Returns (ms per step, host wall ms per step)."""
+    if graph:
+        for i in range(warmup):
+            fn_step(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(steps):
+                fn_step(i)
+        g.replay()  # untimed replay
+        torch.cuda.synchronize()
+        run = g.replay
+    else:
+        for i in range(warmup):
+            fn_step(i)
+
+        def run():
+            for i in range(steps):
+                fn_step(i)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     t0.record(stream)
-    for i in range(steps):
-        fn_step(i, evs[i] if evs else None)
+    run()
     t1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - w0) * 1e3
-    ms = t0.elapsed_time(t1) / steps
-    if not evs:
-        return ms, None, None, wall / steps
-    kms = sorted(a.elapsed_time(b) for a, b in evs)
-    return ms, sum(kms) / len(kms), kms[len(kms) // 2], wall / steps
+    return t0.elapsed_time(t1) / steps, wall / steps
 
 
 def load_traffic(kernel):
@@ -121,20 +132,20 @@ def bench_gemm(torch, ops, wl, stream, steps, warmup):
     d_scale = torch.tensor([1.0 / 64.0], dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
 
-    def step(i, ev):
+    def step(i):
         ops.moe_quant(x, q, qs, PM, K=PK)
         ops.mxfp4_gemm_e4m3(wp, sp, q, qs, c, d_scale, M=PM, m=PN, k=PK)
 
-    def gemm(i, ev):
+    def gemm(i):
         ops.mxfp4_gemm_e4m3(wp, sp, q, qs, c, d_scale, M=PM, m=PN, k=PK)
 
-    def quant(i, ev):
+    def quant(i):
         ops.moe_quant(x, q, qs, PM, K=PK)
 
     log(f"config 3: timing {steps} steps after {warmup} warm-up")
-    ms_step, _, _, wall = timed_loop(torch, stream, step, steps, warmup)
-    k_avg, _, _, _ = timed_loop(torch, stream, gemm, steps, warmup)
-    q_avg, _, _, _ = timed_loop(torch, stream, quant, steps, warmup)
+    ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
+    k_avg, _ = timed_loop(torch, stream, gemm, steps, warmup)
+    q_avg, _ = timed_loop(torch, stream, quant, steps, warmup)
     flop = 2.0 * PM * PN * PK
     q_bytes = PM * PK * 2 + PM * PK + PM * PK // 32
     return {
@@ -159,12 +170,12 @@ def bench_decode(torch, ops, wl, stream, steps, warmup, M):
     y = torch.empty((M, DN), dtype=torch.bfloat16, device="cuda")
     torch.cuda.synchronize()
 
-    def step(i, ev):
+    def step(i):
         wp, sp = ws[i % copies]
         ops.mxfp4_gemv_bf16(x, wp, sp, y, M, N=DN, K=DK)
 
     log(f"config 2: timing {steps} launches after {warmup} warm-up")
-    ms_step, _, _, wall = timed_loop(torch, stream, step, steps, warmup)
+    ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
     nbytes = wbytes + 2 * M * DK + 2 * M * DN
     return {"ms_per_step": ms_step, "kernel_ms": ms_step, "bytes": nbytes,
             "copies": copies, "x": x, "ws": ws}
@@ -204,6 +215,16 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.only == "copy":
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"metric": "plain device copy (counter calibration)", "bytes_read_per_copy": n,
+                          "bytes_written_per_copy": n, "copies": 3}), flush=True)
+        return
     ops.lib()
     stream = torch.cuda.Stream()
     out = {}
@@ -229,6 +250,7 @@ def main():
                             "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                             "traffic": load_traffic("kern_mx_gemv_bf16"),
                             "kernel": "kern_mx_gemv_bf16", "kernel_us": round(d["kernel_ms"] * 1e3, 3),
+
                             "algorithmic_bytes": d["bytes"]},
                "config": {"M": args.decode_m, "N": DN, "K": DK, "weight_copies": d["copies"]}}
 
@@ -246,6 +268,7 @@ def main():
                          "frac": round(kt / PEAK_MXFP4_TFLOPS, 4),
                          "traffic": load_traffic("kern_mx_gemm_e4m3"),
                          "kernel": "kern_mx_gemm_e4m3", "kernel_us": round(g["kernel_ms"] * 1e3, 3),
+
                          "algorithmic_flop": g["flop"],
                          "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4)},
             "quantizer": {"kernel": "kern_mx_quant_bf16", "kernel_us": round(g["quant_ms"] * 1e3, 3),
