@@ -275,6 +275,9 @@ struct Args {
   }
 };
 
+// threads of one GEMM workgroup (8 waves)
+constexpr uint32_t kBmmThreads = 512;
+
 int launch(const char* entry, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, void* stream, Args& a,
            uint32_t shared_bytes = 0) {
   kern_function f = nullptr;
@@ -368,7 +371,7 @@ extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put((void*)c), a.put(num_non_exiting), a.put(total_padded);
   a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(sf_b_r128c4 ? 1 : 0), a.put(dbg);
-  return launch("kern_mx_bmm_fc2", (uint32_t)(m / 256), (uint32_t)ctas, 1, 256, stream, a);
+  return launch("kern_mx_bmm_fc2", (uint32_t)(m / 256), (uint32_t)ctas, 1, kBmmThreads, stream, a);
 }
 
 extern "C" int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a_, const void* sf_a, const void* b,
@@ -387,7 +390,7 @@ extern "C" int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a_, const void* 
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(sf_c), a.put(route_map), a.put(alpha), a.put(beta);
   a.put(num_non_exiting), a.put(total_padded), a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(dbg);
-  return launch("kern_mx_bmm_fc1", (uint32_t)(m / 256), (uint32_t)ctas, 1, 256, stream, a);
+  return launch("kern_mx_bmm_fc1", (uint32_t)(m / 256), (uint32_t)ctas, 1, kBmmThreads, stream, a);
 }
 
 extern "C" int kern_mxfp4_gemm_e4m3(const void* a_, const void* sf_a, const void* b, const void* sf_b, void* c,
@@ -398,7 +401,7 @@ extern "C" int kern_mxfp4_gemm_e4m3(const void* a_, const void* sf_a, const void
   if (M == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(d_scale), a.put(M), a.put(m), a.put(k), a.put(dbg);
-  return launch("kern_mx_gemm_e4m3", (uint32_t)(m / 256), (uint32_t)((M + 127) / 128), 1, 256, stream, a);
+  return launch("kern_mx_gemm_e4m3", (uint32_t)(m / 256), (uint32_t)((M + 127) / 128), 1, kBmmThreads, stream, a);
 }
 
 extern "C" int kern_mxfp4_gemm_bf16(const void* a_, const void* sf_a, const void* b, const void* sf_b, void* c,
@@ -409,7 +412,7 @@ extern "C" int kern_mxfp4_gemm_bf16(const void* a_, const void* sf_a, const void
   if (M == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(M), a.put(m), a.put(k), a.put(dbg);
-  return launch("kern_mx_gemm_bf16", (uint32_t)(m / 256), (uint32_t)((M + 127) / 128), 1, 256, stream, a);
+  return launch("kern_mx_gemm_bf16", (uint32_t)(m / 256), (uint32_t)((M + 127) / 128), 1, kBmmThreads, stream, a);
 }
 
 extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_sf, void* y, int32_t M, int32_t N,

@@ -222,10 +222,13 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 }
 
 // ====================================================================================== block-scaled GEMM
-// One workgroup computes a 128-row (token/slot) x 256-row (weight) tile with 4 waves in a 2x2 grid; each
-// wave owns 64 x 128 = 4 x 8 tiles of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (A = fp4 weights, B = e4m3
-// activations, e8m0 scales in-instruction). K advances in 128-wide k-tiles through a four-stage LDS ring
-// filled by direct global->LDS loads (GLOBAL_LOAD_LDS_DWORDX4), three tiles ahead of the MFMAs:
+// One workgroup computes a 128-row (token/slot) x 256-row (weight) tile with 8 waves (two per SIMD) in a
+// 2x4 grid; each wave owns 64 x 64 = 4 x 4 tiles of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (A = fp4 weights,
+// B = e4m3 activations, e8m0 scales in-instruction). K advances in 128-wide k-tiles through a four-stage
+// LDS ring filled by direct global->LDS loads (GLOBAL_LOAD_LDS_DWORDX4), up to four tiles ahead of the
+// MFMAs. Each k-step multiplies half of its tile, meets the other waves at the step's one barrier,
+// refills the stage it has just finished reading, reads the next tile's operands and multiplies the
+// other half while those reads land; the second wave of each SIMD fills the first one's stalls.
 //   W stage: 16 fragments of 1 KiB, copied verbatim (the repacked layout is the MFMA operand layout);
 //   X stage: 128 rows x 128 B, 16-byte chunk j of row t stored at t*128 + ((j ^ ((t>>1)&7)) << 4) so that
 //      the fragment reads (16 rows, one chunk each) touch distinct bank groups; the permutation is
@@ -273,6 +276,8 @@ KERN_DEV void dma4(const void* g, void* lds_wave_base) {
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
 // lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | 0x70 | 0xF00 | (((n) >> 4) << 14))
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left alone
+#define WAIT_LGKMCNT0 __builtin_amdgcn_s_waitcnt(0xC07F)
 
 // The LDS ring. Each stage and scale slot is its own variable, so that the compiler's wait-count
 // analysis can tell a read of one stage from the loads still landing in another.
@@ -288,7 +293,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   // the wave index through readfirstlane: provably uniform, so everything derived from it (the LDS
   // bases of the direct loads) lives in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wt = wave >> 1, wn = wave & 1;
+  const int wt = wave >> 2, wn = wave & 3;  // token half, weight quarter
   const int gx = A.m / BN;
   // XCD-aware linearisation: consecutive workgroups land on different XCDs (round robin over 8); give
   // each XCD a contiguous run of tiles so that its L2 sees the reuse.
@@ -321,156 +326,198 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
     if (MODE == MODE_FC1) return A.route_map[row0 + t];
     return row0 + t;
   };
-  // X tile DMA: instruction r of this wave fills LDS rows 32r + 8*wave + lane/8, position lane%8
+  // Two wave groups take turns (ping-pong): group 0 (waves 0-3, token rows 0-63) brings in the weight
+  // tiles, group 1 (waves 4-7, rows 64-127) the activation tiles; waves w and w+4 share a SIMD. Every
+  // k-tile t has two half-steps separated by workgroup barriers: in the first, group 0 multiplies tile t
+  // while group 1 requests activations three tiles ahead and reads tile t's operands; in the second,
+  // group 1 multiplies tile t while group 0 requests weights four tiles ahead and reads tile t+1's
+  // operands. Each SIMD's matrix core thus always has one wave's MFMAs queued while the other wave's
+  // loads are in flight.
+  const int grp = wt, gw = wn;
+  // group 1: activation request r fills LDS rows 32r + 8*gw + lane/8, position lane%8
   const int xpos = lane & 7;
   const uint8_t* xsrc[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int t = 32 * r + 8 * wave + (lane >> 3);
+    const int t = 32 * r + 8 * gw + (lane >> 3);
     xsrc[r] = A.b + token_of(t) * K + ((xpos ^ ((t >> 1) & 7)) << 4);
   }
-  // X scale DMA (dwords): this lane's row (64*wave + lane) & 127; instruction r covers k-tile 2r + wave/2
-  const int64_t srow = token_of((64 * wave + lane) & 127);
-  auto sx_src = [&](int kg, int r) -> const uint8_t* {
-    const int kt = kg * 4 + 2 * r + (wave >> 1);
+  // group 1: activation scale dwords, rows 64h + lane of k-tile gw of a group; address of k-tile 0's dword
+  // and the step between k-tiles: linear [T][K/32] or R128c4 (one 512-byte tile per 128 rows x 4 k blocks)
+  const uint8_t* sx_row[2];
+  int sx_step;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t srow = token_of(64 * h + lane);
     if (A.sf_b_r128c4) {
       const int64_t kb4 = K >> 7;  // ceil(kblocks/4) with K % 128 == 0
-      return A.sf_b + 512 * ((srow >> 7) * kb4 + kt) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
+      sx_row[h] = A.sf_b + 512 * ((srow >> 7) * kb4) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
+    } else {
+      sx_row[h] = A.sf_b + srow * (K >> 5);
     }
-    return A.sf_b + srow * (K >> 5) + kt * 4;
-  };
+  }
+  sx_step = A.sf_b_r128c4 ? 512 : 4;
 
-  // requests of one tile (8 per wave) and of one k group's scales (3 per wave); indices past the end are
-  // clamped to the last tile / group, whose data is then never multiplied
-  auto dma_tile = [&](int kt, uint8_t* sW, uint8_t* sX) {
+  // requests (indices past the end are clamped to the last tile / group, whose data is then never
+  // multiplied): group 0 issues 4 per weight tile and 4 per weight-scale group, group 1 4 per activation
+  // tile and 2 per activation-scale group
+  auto dma_w_tile = [&](int kt, uint8_t* sW) {
     kt = min(kt, KT - 1);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int f = r * 4 + wave;  // fragment (row group) 0..15
+      const int f = r * 4 + gw;  // fragment (16-row group) 0..15
       dma16(wbase + ((int64_t)f * KT + kt) * 1024 + lane * 16, sW + f * 1024);
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dma16(xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + wave) * 1024);
   };
-  auto dma_scales = [&](int kg, uint8_t* sSW, uint8_t* sSX) {
+  auto dma_w_scales = [&](int kg, uint8_t* sSW) {
     kg = min(kg, KG - 1);
-    const int f = 4 * wave + (lane >> 4);
-    dma16(sbase + ((int64_t)f * KG + kg) * 256 + (lane & 15) * 16, sSW + 1024 * wave);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) dma4(sx_src(kg, r), sSX + 4 * (r * 4 + wave) * 64);
+    for (int r = 0; r < 4; ++r) {
+      const int f = r * 4 + gw;
+      dma4(sbase + ((int64_t)f * KG + kg) * 256 + lane * 4, sSW + f * 256);
+    }
+  };
+  auto dma_x_tile = [&](int kt, uint8_t* sX) {
+    kt = min(kt, KT - 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dma16(xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
+  };
+  auto dma_x_scales = [&](int kg, uint8_t* sSX) {
+    kg = min(kg, KG - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) dma4(sx_row[h] + (int64_t)(kg * 4 + gw) * sx_step, sSX + 4 * (gw * BT + 64 * h));
   };
 
-  v4f acc[4][8];
+  v4f acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   // number of live 16-row token subtiles for this wave
   const int live_ts = min(4, max(0, (valid - wt * 64 + 15) >> 4));
   const int c = lane & 15, g = lane >> 4;
 
-  // prologue: scales of group 0, tiles 0..2 in flight; wait for the scales and tile 0
-  dma_scales(0, L.sw[0], L.sx[0]);
-  dma_tile(0, L.w[0], L.x[0]);
-  dma_tile(1, L.w[1], L.x[1]);
-  dma_tile(2, L.w[2], L.x[2]);
-  WAIT_VMCNT(16);
+  // prologue: group 0 requests the weight scales of group 0 and weight tiles 0..3, group 1 the activation
+  // scales and activation tiles 0..2; tile 0 and the scales have landed once the later tiles' requests
+  // alone are outstanding
+  if (grp == 0) {
+    dma_w_scales(0, L.sw[0]);
+    dma_w_tile(0, L.w[0]);
+    dma_w_tile(1, L.w[1]);
+    dma_w_tile(2, L.w[2]);
+    dma_w_tile(3, L.w[3]);
+    WAIT_VMCNT(12);
+  } else {
+    dma_x_scales(0, L.sx[0]);
+    dma_x_tile(0, L.x[0]);
+    dma_x_tile(1, L.x[1]);
+    dma_x_tile(2, L.x[2]);
+    WAIT_VMCNT(8);
+  }
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
   auto run = [&](auto NTSc) {
     constexpr int NTS = decltype(NTSc)::value;  // live token subtiles of this wave (uniform)
-    v4i wa[2][8];       // W operands of tile kt (set kt&1) and kt+1
-    v8i xbuf[2];        // X operand of the current and the next subtile
-    uint32_t sxv[2];    // X scale dwords of the same
-    uint32_t swd[8], swn[8];  // weight-scale dwords of the current and the next k group
-    auto read_w = [&](const uint8_t* sW, int set) {
+    v4i wa[4];         // W operands of the tile in hand
+    v8i xb[4];         // X operands, per token subtile
+    uint32_t sxv[4];   // X scale bytes
+    uint32_t swd[4];   // weight-scale dwords of the current k group
+    // operands of the tile in stage st (k-tile jt of its group; weight scales too when jt == 0)
+    auto read_tile = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sSW, const uint8_t* sSX, int jt,
+                         bool with_sw) {
 #pragma unroll
-      for (int rs = 0; rs < 8; ++rs) wa[set][rs] = *reinterpret_cast<const v4i*>(sW + (wn * 8 + rs) * 1024 + lane * 16);
-    };
-    auto read_x = [&](const uint8_t* sX, const uint8_t* sSX, int jt, int ts, int xs) {
-      const int t = wt * 64 + ts * 16 + c;
-      const uint8_t* xr = sX + t * 128;
-      const int sw = (t >> 1) & 7;
-      const v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
-      const v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
-      xbuf[xs] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      sxv[xs] = reinterpret_cast<const uint32_t*>(sSX)[jt * BT + t] >> (8 * g);
-    };
-    auto read_sw = [&](const uint8_t* sSW, uint32_t* dst) {
+      for (int rs = 0; rs < 4; ++rs) wa[rs] = *reinterpret_cast<const v4i*>(sW + (wn * 4 + rs) * 1024 + lane * 16);
+      if (with_sw) {
 #pragma unroll
-      for (int rs = 0; rs < 8; ++rs) dst[rs] = reinterpret_cast<const uint32_t*>(sSW + (wn * 8 + rs) * 256)[lane];
+        for (int rs = 0; rs < 4; ++rs) swd[rs] = reinterpret_cast<const uint32_t*>(sSW + (wn * 4 + rs) * 256)[lane];
+      }
+#pragma unroll
+      for (int ts = 0; ts < NTS; ++ts) {
+        const int t = wt * 64 + ts * 16 + c;
+        const uint8_t* xr = sX + t * 128;
+        const int sw = (t >> 1) & 7;
+        const v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
+        const v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
+        xb[ts] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        // the scale byte of this lane's 32-wide k block, read as a byte so that no shift waits on it
+        sxv[ts] = sSX[(jt * BT + t) * 4 + g];
+      }
     };
-    auto mfmas = [&](int set, int ts, int xs, auto Jt) {
+    auto mfmas = [&](auto Jt) {
       constexpr int jt = decltype(Jt)::value;  // k-tile within the group: scale byte of the weights
 #pragma unroll
-      for (int rs = 0; rs < 8; ++rs) {
-        const v8i wb = {wa[set][rs][0], wa[set][rs][1], wa[set][rs][2], wa[set][rs][3], 0, 0, 0, 0};
-        acc[ts][rs] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xbuf[xs], acc[ts][rs], 4, 0, jt,
-                                                                        (int)swd[rs], 0, (int)sxv[xs]);
-      }
-    };
-
-    read_sw(L.sw[0], swd);
-    read_w(L.w[0], 0);
-    if (NTS > 0) read_x(L.x[0], L.sx[0], 0, 0, 0);
-
-    // step J of a pair of k groups: tile kt = 8*kk + J, stage kt % 4 = J % 4, scale slot = J / 4
-    auto step = [&](int kk, auto Jc) {
-      constexpr int J = decltype(Jc)::value;
-      constexpr int jt = J & 3, st = J & 3, sb = J >> 2;
-      constexpr int cur = J & 1, nxt = cur ^ 1;
-      constexpr int st1 = (st + 1) & 3, st3 = (st + 3) & 3;
-      constexpr int sb1 = jt == 3 ? sb ^ 1 : sb;  // scale slot of tile kt+1
-      const int kt = kk * 8 + J;
-      const int kg = kt >> 2;
-      // phase 0: requests for later tiles (the stage of tile kt+3 was last read before the previous
-      // barrier), then the first subtile
-      if (jt == 0) dma_scales(kg + 1, L.sw[sb ^ 1], L.sx[sb ^ 1]);
-      dma_tile(kt + 3, L.w[st3], L.x[st3]);
-      if (NTS > 1) read_x(L.x[st], L.sx[sb], jt, 1, 1);
-      if (NTS > 0) mfmas(cur, 0, 0, IC<jt>{});
-      __builtin_amdgcn_sched_barrier(0);
-      // phases 1, 2
-      if (NTS > 2) read_x(L.x[st], L.sx[sb], jt, 2, 0);
-      if (NTS > 1) mfmas(cur, 1, 1, IC<jt>{});
-      __builtin_amdgcn_sched_barrier(0);
-      if (NTS > 3) read_x(L.x[st], L.sx[sb], jt, 3, 1);
-      if (NTS > 2) mfmas(cur, 2, 0, IC<jt>{});
-      __builtin_amdgcn_sched_barrier(0);
-      // tile kt+1 (requested in step kt-2) has landed for this wave once at most the requests issued
-      // after it are outstanding: tiles kt+2, kt+3 (8 each) and the scales requested in steps kt-1, kt
-      WAIT_VMCNT(16 + (jt == 1 ? 3 : 0) + (jt == 0 ? 3 : 0));
-      __builtin_amdgcn_s_barrier();  // ... and for every wave; every read of stage kt%4's subtiles 1-3 is issued
-      __builtin_amdgcn_sched_barrier(0);
-      // phase 3: operands of tile kt+1 (the first tile of group kg+1 when jt == 3)
-      read_w(L.w[st1], nxt);
-      if (jt == 3) read_sw(L.sw[sb1], swn);
-      if (NTS > 0) read_x(L.x[st1], L.sx[sb1], (jt + 1) & 3, 0, 0);
-      if (NTS > 3) mfmas(cur, 3, 1, IC<jt>{});
-      if (jt == 3) {
+      for (int ts = 0; ts < NTS; ++ts)
 #pragma unroll
-        for (int rs = 0; rs < 8; ++rs) swd[rs] = swn[rs];
-      }
+        for (int rs = 0; rs < 4; ++rs) {
+          const v8i wb = {wa[rs][0], wa[rs][1], wa[rs][2], wa[rs][3], 0, 0, 0, 0};
+          acc[ts][rs] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb[ts], acc[ts][rs], 4, 0, jt,
+                                                                          (int)swd[rs], 0, (int)sxv[ts]);
+        }
+    };
+    // k-tile t = 8*kk + J lives in stage J % 4; its group's scales in slot J / 4 (group parity)
+    auto step0 = [&](int kk, auto Jc) {  // group 0
+      constexpr int J = decltype(Jc)::value;
+      constexpr int jt = J & 3, st = J & 3, st1 = (J + 1) & 3, sb = J >> 2, sb1 = ((J + 1) >> 2) & 1;
+      const int kt = kk * 8 + J, kg = kt >> 2;
+      // first half-step: multiply tile kt (operands read in the previous half-step)
+      mfmas(IC<jt>{});
+      __builtin_amdgcn_sched_barrier(0);
+      // this wave's weights of tile kt+1 have landed once at most tiles kt+2, kt+3 and the scales
+      // requested with them are outstanding
+      WAIT_VMCNT(8 + ((jt == 1 || jt == 2) ? 4 : 0));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // second half-step: stage kt%4 is read by both groups; refill it with weight tile kt+4 (the next
+      // group's weight scales first), then read tile kt+1
+      if (jt == 0) dma_w_scales(kg + 1, L.sw[sb ^ 1]);
+      dma_w_tile(kt + 4, L.w[st]);
+      read_tile(L.w[st1], L.x[st1], L.sw[sb1], L.sx[sb1], (jt + 1) & 3, jt == 3);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto step1 = [&](int kk, auto Jc) {  // group 1
+      constexpr int J = decltype(Jc)::value;
+      constexpr int jt = J & 3, st = J & 3, st3 = (J + 3) & 3, sb = J >> 2;
+      const int kt = kk * 8 + J, kg = kt >> 2;
+      // first half-step: activation tile kt+3 into stage (kt+3)%4 (the next group's activation scales
+      // first when kt+3 starts it), then this tile's operands, complete before the barrier because
+      // group 0 refills the stage next
+      if (jt == 1) dma_x_scales(kg + 1, L.sx[sb ^ 1]);
+      dma_x_tile(kt + 3, L.x[st3]);
+      read_tile(L.w[st], L.x[st], L.sw[sb], L.sx[sb], jt, jt == 0);
+      WAIT_LGKMCNT0;
+      // this wave's activations of tile kt+1 have landed once at most tiles kt+2, kt+3 and the scales
+      // requested with them are outstanding
+      WAIT_VMCNT(8 + ((jt == 1 || jt == 2) ? 2 : 0));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // second half-step: multiply tile kt
+      mfmas(IC<jt>{});
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     };
     const int pairs = KG >> 1;
-    for (int kk = 0; kk < pairs; ++kk) {
-      step(kk, IC<0>{});
-      step(kk, IC<1>{});
-      step(kk, IC<2>{});
-      step(kk, IC<3>{});
-      step(kk, IC<4>{});
-      step(kk, IC<5>{});
-      step(kk, IC<6>{});
-      step(kk, IC<7>{});
-    }
-    if (KG & 1) {  // last (even-numbered) group
-      step(pairs, IC<0>{});
-      step(pairs, IC<1>{});
-      step(pairs, IC<2>{});
-      step(pairs, IC<3>{});
+    if (grp == 0) {
+      read_tile(L.w[0], L.x[0], L.sw[0], L.sx[0], 0, true);
+      for (int kk = 0; kk < pairs; ++kk) {
+        step0(kk, IC<0>{}); step0(kk, IC<1>{}); step0(kk, IC<2>{}); step0(kk, IC<3>{});
+        step0(kk, IC<4>{}); step0(kk, IC<5>{}); step0(kk, IC<6>{}); step0(kk, IC<7>{});
+      }
+      if (KG & 1) {  // last (even-numbered) group
+        step0(pairs, IC<0>{}); step0(pairs, IC<1>{}); step0(pairs, IC<2>{}); step0(pairs, IC<3>{});
+      }
+    } else {
+      for (int kk = 0; kk < pairs; ++kk) {
+        step1(kk, IC<0>{}); step1(kk, IC<1>{}); step1(kk, IC<2>{}); step1(kk, IC<3>{});
+        step1(kk, IC<4>{}); step1(kk, IC<5>{}); step1(kk, IC<6>{}); step1(kk, IC<7>{});
+      }
+      if (KG & 1) {
+        step1(pairs, IC<0>{}); step1(pairs, IC<1>{}); step1(pairs, IC<2>{}); step1(pairs, IC<3>{});
+      }
     }
   };
   switch (live_ts) {
@@ -484,7 +531,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   WAIT_VMCNT(0);
 
   // ---- epilogue: lane (c, g) of tile (ts, rs) holds weight rows 16*rs + 4*g + i, token row c
-  const int wrow0 = nx * BN + wn * 128;  // first weight row of this wave
+  const int wrow0 = nx * BN + wn * 64;  // first weight row of this wave
   if (MODE == MODE_FC2 || MODE == MODE_DENSE_BF16) {
     uint16_t* C = reinterpret_cast<uint16_t*>(A.c);
 #pragma unroll
@@ -493,7 +540,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
       if (t < valid) {
         const int64_t p = row0 + t;
 #pragma unroll
-        for (int rs = 0; rs < 8; ++rs) {
+        for (int rs = 0; rs < 4; ++rs) {
           const int n = wrow0 + rs * 16 + g * 4;
           const v4f v = acc[ts][rs];
           if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
@@ -512,7 +559,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
       if (t < valid) {
         const int64_t p = row0 + t;
 #pragma unroll
-        for (int rs = 0; rs < 8; ++rs) {
+        for (int rs = 0; rs < 4; ++rs) {
           const int n = wrow0 + rs * 16 + g * 4;
           const v4f v = acc[ts][rs];
           if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
@@ -525,14 +572,16 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
     uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
     const int half = m >> 1;
     const float al = A.alpha[expert], be = A.beta[expert];
-    const int ncol0 = (nx * BN + wn * 128) >> 1;  // first output column of this wave (64 of them)
+    // the wave's 64 interleaved gate/up rows give 32 output columns: one MXFP8 block
+    const int ncol0 = (nx * BN + wn * 64) >> 1;
+    const int blk = ncol0 >> 5;
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       const int t = wt * 64 + ts * 16 + c;
-      // h for 8 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
-      float h[8][2];
+      // h for 4 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
+      float h[4][2];
 #pragma unroll
-      for (int rs = 0; rs < 8; ++rs) {
+      for (int rs = 0; rs < 4; ++rs) {
         const v4f v = acc[ts][rs];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -545,7 +594,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
       const int64_t p = row0 + t;
       if (ok && A.dbg) {
 #pragma unroll
-        for (int rs = 0; rs < 8; ++rs)
+        for (int rs = 0; rs < 4; ++rs)
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             const int n = ncol0 + 8 * rs + 2 * g + i;
@@ -554,30 +603,25 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
             A.dbg[(p * 3 + 2) * half + n] = h[rs][i];
           }
       }
-      // two 32-column blocks: subtiles 0-3 and 4-7
+      uint32_t amax = 0;
 #pragma unroll
-      for (int bk = 0; bk < 2; ++bk) {
-        uint32_t amax = 0;
+      for (int rs = 0; rs < 4; ++rs)
 #pragma unroll
-        for (int rs = 0; rs < 4; ++rs)
+        for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[rs][i]) & 0x7fffffffu);
+      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
+      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
+      const uint32_t sc = mx_scale_code(amax);
+      if (ok) {
 #pragma unroll
-          for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[bk * 4 + rs][i]) & 0x7fffffffu);
-        amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
-        amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
-        const uint32_t sc = mx_scale_code(amax);
-        if (ok) {
-#pragma unroll
-          for (int rs = 0; rs < 4; ++rs) {
-            const int n = ncol0 + 8 * (bk * 4 + rs) + 2 * g;
-            const uint32_t o = mx_code2(h[bk * 4 + rs][0], h[bk * 4 + rs][1], sc);
-            *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
-          }
-          if (g == 0) {
-            const int blk = (ncol0 >> 5) + bk;
-            const int64_t kb4 = ((half >> 5) + 3) >> 2;
-            const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
-            A.sf_c[off] = (uint8_t)sc;
-          }
+        for (int rs = 0; rs < 4; ++rs) {
+          const int n = ncol0 + 8 * rs + 2 * g;
+          const uint32_t o = mx_code2(h[rs][0], h[rs][1], sc);
+          *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
+        }
+        if (g == 0) {
+          const int64_t kb4 = ((half >> 5) + 3) >> 2;
+          const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
+          A.sf_c[off] = (uint8_t)sc;
         }
       }
     }
@@ -594,8 +638,8 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
 // a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
 // cta_batch, cta_limit; launch adds i32 m, i32 k, i32 sf_b_r128c4, f32* dbg (may be null).
-// Grid [m/256, slots, 1], block 256; slot y >= num_non_exiting[0] exits.
-extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2(
+// Grid [m/256, slots, 1], block 512; slot y >= num_non_exiting[0] exits.
+extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
     const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
     int sf_b_r128c4, float* dbg) {
@@ -610,8 +654,8 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2(
 
 // op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
 // c u8 [padded][m/2], sf_c u8 R128c4, route_map, alpha, beta, num_non_exiting, total_padded, cta_batch,
-// cta_limit; launch adds i32 m, i32 k, f32* dbg. Grid [m/256, slots, 1], block 256.
-extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc1(
+// cta_limit; launch adds i32 m, i32 k, f32* dbg. Grid [m/256, slots, 1], block 512.
+extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
     const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
     const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, float* dbg) {
@@ -627,8 +671,8 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc1(
 
 // Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).
 // a, sf_a, b [M][k], sf_b linear, c u8 [M][m], d_scale f32[1], i32 M; launch adds i32 m, i32 k, f32* dbg.
-// Grid [m/256, ceil(M/128), 1], block 256.
-extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_e4m3(const uint8_t* a, const uint8_t* sf_a,
+// Grid [m/256, ceil(M/128), 1], block 512.
+extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_e4m3(const uint8_t* a, const uint8_t* sf_a,
                                                                     const uint8_t* b, const uint8_t* sf_b,
                                                                     uint8_t* c, const float* d_scale, int M, int m,
                                                                     int k, float* dbg) {
@@ -640,7 +684,7 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_e4m3(const uint8_
 }
 
 // Dense bf16-output mode of the FC2 family (one batch, no routing tables).
-extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_bf16(const uint8_t* a, const uint8_t* sf_a,
+extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_bf16(const uint8_t* a, const uint8_t* sf_a,
                                                                     const uint8_t* b, const uint8_t* sf_b,
                                                                     uint16_t* c, int M, int m, int k, float* dbg) {
   BMM_LDS_DECL(L);
