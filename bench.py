@@ -1,6 +1,6 @@
 """Benchmark of the MXFP4 matmul path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemm|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemm|decode|moe|copy]
 
 Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
 
@@ -17,6 +17,11 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
 * `decode` = config 2 at M=1: W4A16 GEMV over [18432, 7168] MXFP4 weights, rotating over enough weight
   copies (> 256 MB, the Infinity Cache) that every launch streams its weights from HBM; GB/s of
   algorithmic bytes against the 8 TB/s HBM peak.
+* `moe` = config 4: T=512 tokens, 256 experts, top-8, H=7168, I=2048. One step = moe_quant of the tokens,
+  moe_routing, FC1 (gate+up K=7168 -> 2I=4096, SiTU-GLU, MXFP8 out) and FC2 (K=2048 -> 7168, bf16 out),
+  with ~6 GB of repacked weights (every expert is hit), so each step streams its weights from HBM; GB/s of
+  algorithmic bytes (weights of the experts hit + routed activations in and out) against the HBM peak,
+  for the step and for FC1 and FC2 alone.
 * `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on a bounded
   sample of the same GEMM (its first rows), in the headline unit.
 * `traffic` comes from committed rocprofv3 --pmc summaries (profiles/traffic.json), null without one.
@@ -42,6 +47,8 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
 # config 3 (prefill GEMM) and config 2 (decode GEMV) shapes, BASELINE.json configs[2] / configs[1]
 PM, PN, PK = 4096, 2048, 7168
 DN, DK = 18432, 7168
+# config 4 (MoE grouped)
+MT, ME, MTOP, MH, MI = 512, 256, 8, 7168, 2048
 MALL_BYTES = 256 << 20
 
 
@@ -51,7 +58,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["gemm", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "decode", "moe", "copy"], default=None,
                     help="run one leg only (for profiling); the JSON line then carries that leg. 'copy' runs "
                          "three plain 256 MiB device copies: the reference for scaling HBM byte counters")
     ap.add_argument("--decode-m", type=int, default=1)
@@ -181,6 +188,71 @@ def bench_decode(torch, ops, wl, stream, steps, warmup, M):
             "copies": copies, "x": x, "ws": ws}
 
 
+def bench_moe(torch, ops, wl, stream, steps, warmup):
+    log(f"config 4: T={MT} E={ME} top-{MTOP} H={MH} I={MI}: generating weights")
+    u8 = torch.uint8
+    x = dev_from_np(wl.activations_bf16(4, MT, MH), torch)
+    ids_np = wl.topk_ids(4, MT, ME, MTOP)
+    ids = torch.from_numpy(ids_np).cuda()
+
+    def weights(seed, rows, K, gated):
+        w_raw = torch.empty((ME, rows, K // 2), dtype=u8, device="cuda")
+        s_raw = torch.empty((ME, rows, K // 32), dtype=u8, device="cuda")
+        ops.fill_random_u8(w_raw, wl.tensor_seed(seed, 3))
+        ops.fill_random_u8(s_raw, wl.tensor_seed(seed, 4), 119, 6)
+        out = ops.repack_weights(w_raw, s_raw, gated=gated)  # load-time derive, not part of a step
+        del w_raw, s_raw
+        return out
+
+    w1, s1 = weights(40, 2 * MI, MH, True)
+    w2, s2 = weights(41, MH, MI, False)
+    alpha = torch.full((ME,), 4.0, dtype=torch.float32, device="cuda")
+    beta = torch.full((ME,), 25.0, dtype=torch.float32, device="cuda")
+    ctas = ops.ctas_bound(MT, MTOP, ME)
+    rows = ctas * 128
+    i32 = torch.int32
+    tab = {n: torch.zeros(sz, dtype=i32, device="cuda") for n, sz in
+           [("counts", 2 * ME), ("cta_batch", ctas), ("cta_limit", ctas), ("nne", 1), ("total_padded", 1),
+            ("route_map", rows), ("exp2perm", MT * MTOP)]}
+    q = torch.empty((MT, MH), dtype=u8, device="cuda")
+    qs = torch.empty((MT, MH // 32), dtype=u8, device="cuda")
+    c1 = torch.empty((rows, MI), dtype=u8, device="cuda")
+    sf1 = torch.empty((rows // 128) * 512 * (-(-(MI // 32) // 4)), dtype=u8, device="cuda")  # R128c4
+    c2 = torch.empty((rows, MH), dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+
+    def route():
+        ops.moe_quant(x, q, qs, MT, K=MH)
+        ops.moe_routing(ids, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"], tab["total_padded"],
+                        tab["route_map"], tab["exp2perm"], tokens=MT, topk=MTOP, local_start=0, local_experts=ME)
+
+    def fc1():
+        ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(w1, s1, q, qs, c1, sf1, tab["route_map"], alpha, beta, tab["nne"],
+                                            tab["total_padded"], tab["cta_batch"], tab["cta_limit"], m=2 * MI,
+                                            k=MH, ctas=ctas)
+
+    def fc2():
+        ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(w2, s2, c1, sf1, c2, tab["nne"], tab["total_padded"], tab["cta_batch"],
+                                          tab["cta_limit"], m=MH, k=MI, ctas=ctas, sf_b_r128c4=True)
+
+    def step(i):
+        route()
+        fc1()
+        fc2()
+
+    log(f"config 4: timing {steps} steps after {warmup} warm-up")
+    ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
+    ms_fc1, _ = timed_loop(torch, stream, lambda i: fc1(), steps, warmup)
+    ms_fc2, _ = timed_loop(torch, stream, lambda i: fc2(), steps, warmup)
+    hit = len(set(ids_np.reshape(-1).tolist()))
+    R = MT * MTOP
+    b_fc1 = hit * 2 * MI * MH * 17 // 32 + R * MH * 33 // 32 + R * MI * 33 // 32
+    b_fc2 = hit * MH * MI * 17 // 32 + R * MI * 33 // 32 + R * MH * 2
+    b_step = b_fc1 + b_fc2 + MT * MH * 2 + MT * MH * 33 // 32 + MT * MTOP * 4
+    return {"ms_per_step": ms_step, "wall_ms_per_step": wall, "ms_fc1": ms_fc1, "ms_fc2": ms_fc2,
+            "bytes_fc1": b_fc1, "bytes_fc2": b_fc2, "bytes_step": b_step, "experts_hit": hit, "slots": ctas}
+
+
 def cpu_baseline_gemm(torch, wl, tensors):
     """The C oracle on the first rows of the same GEMM (bounded sample), fp32 accumulation."""
     import numpy as np
@@ -229,11 +301,15 @@ def main():
     stream = torch.cuda.Stream()
     out = {}
     with torch.cuda.stream(stream):
-        g = d = None
+        g = d = mo = None
         if args.only in (None, "gemm"):
             g = bench_gemm(torch, ops, wl, stream, args.steps, args.warmup)
         if args.only in (None, "decode"):
             d = bench_decode(torch, ops, wl, stream, args.steps, args.warmup, args.decode_m)
+            d.pop("ws")
+        torch.cuda.synchronize()
+        if args.only in (None, "moe"):
+            mo = bench_moe(torch, ops, wl, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
 
     cpu = None
@@ -253,6 +329,23 @@ def main():
 
                             "algorithmic_bytes": d["bytes"]},
                "config": {"M": args.decode_m, "N": DN, "K": DK, "weight_copies": d["copies"]}}
+
+    moe = None
+    if mo is not None:
+        def hbm(nbytes, ms, kernel):
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(kernel), "kernel": kernel,
+                    "kernel_us": round(ms * 1e3, 3), "algorithmic_bytes": nbytes}
+        gbs = mo["bytes_step"] / (mo["ms_per_step"] * 1e-3) / 1e9
+        moe = {"metric": "MoE grouped step GB/s (config 4)", "value": round(gbs, 1), "unit": "GB/s",
+               "ms_per_step": round(mo["ms_per_step"], 5), "frac": round(gbs / PEAK_HBM_GBS, 4),
+               "algorithmic_bytes": mo["bytes_step"],
+               "step": "moe_quant + moe_routing + moe_fc1 + moe_fc2",
+               "fc1": hbm(mo["bytes_fc1"], mo["ms_fc1"], "kern_mx_bmm_fc1"),
+               "fc2": hbm(mo["bytes_fc2"], mo["ms_fc2"], "kern_mx_bmm_fc2"),
+               "config": {"T": MT, "E": ME, "topk": MTOP, "H": MH, "I": MI, "experts_hit": mo["experts_hit"],
+                          "cta_slots": mo["slots"]}}
 
     if g is not None:
         value = g["flop"] / (g["ms_per_step"] * 1e-3) / 1e12
@@ -275,10 +368,11 @@ def main():
                           "GB/s": round(g["quant_bytes"] / (g["quant_ms"] * 1e-3) / 1e9, 1),
                           "algorithmic_bytes": g["quant_bytes"]},
             "decode": dec,
+            "moe": moe,
             "cpu_baseline": cpu,
         }
     else:
-        out = dict(dec)
+        out = dict(dec if dec is not None else moe)
         out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
                     "scaling": "weak", "vs_baseline": None, "dtype": "bf16xmxfp4->f32", "data": "synthetic"})
     print(json.dumps(out), flush=True)

@@ -417,8 +417,8 @@ extern "C" int kern_mxfp4_gemm_bf16(const void* a_, const void* sf_a, const void
 
 extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_sf, void* y, int32_t M, int32_t N,
                                     int32_t K, void* stream) {
-  REQUIRE(M >= 1 && M <= 16 && N > 0 && N % 16 == 0 && K > 0 && K % 512 == 0,
-          "mxfp4_gemv_bf16: need 1 <= M <= 16, N %% 16 == 0, K %% 512 == 0 (M=%d N=%d K=%d)", M, N, K);
+  REQUIRE(M >= 1 && M <= 16 && N > 0 && N % 16 == 0 && K > 0 && K % 512 == 0 && K <= 16384,
+          "mxfp4_gemv_bf16: need 1 <= M <= 16, N %% 16 == 0, K %% 512 == 0, K <= 16384 (M=%d N=%d K=%d)", M, N, K);
   REQUIRE(x && w && w_sf && y, "mxfp4_gemv_bf16: null buffer");
   // sb: k-tiles per wave whose slice of x is staged in LDS at once (at most four 16-byte pieces per lane,
   // M * sb <= 16, sb divides K/512); nb: k-tiles per wave whose weights are in flight together (the
@@ -436,7 +436,8 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
       nb = cand;
       break;
     }
-  const uint32_t lds = (uint32_t)(M + 1) * (uint32_t)(sb * 1024 + 16);  // x slice + one zero row
+  // the x slice of every token, then the row group's scales (256 B per 512 of K)
+  const uint32_t lds = (uint32_t)M * (uint32_t)(sb * 1024 + 16) + (uint32_t)(kq * 256);
   Args a;
   a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K), a.put(nb), a.put(sb);
   return launch("kern_mx_gemv_bf16", (uint32_t)(N / 16), 1, 1, 256, stream, a, lds);

@@ -100,50 +100,74 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_sf_shuffle(const uint8
   reinterpret_cast<uint32_t*>(out)[d] = v;
 }
 
+// LDS and global address spaces (operands of the direct global->LDS loads)
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glob_void_t;
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+// lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | 0x70 | 0xF00 | (((n) >> 4) << 14))
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left alone
+#define WAIT_LGKMCNT0 __builtin_amdgcn_s_waitcnt(0xC07F)
+
 // ====================================================================================== decode GEMV
 // op mxfp4_gemv_bf16 (new; the W4A16 decode of BASELINE configs 1-2): in bf16 x[M][K], in u8 w (repacked,
-// non-gated) [N][K/2], in u8 w_sf (repacked), out bf16 y[M][N], i32 M, launch i32 N, i32 K, i32 nb.
-// Grid N/16, block 256, dynamic LDS (M+1)*(nb*1024 + 16) bytes: one 16-row group per workgroup. Wave w
-// takes the 128-wide k-tiles kt = 4i + w (equal shares; its scales are byte w of the group's scale
-// dwords). Tiles are consumed in batches of nb per wave (nb divides K/512 and M*nb <= 16). Per batch,
-// every lane first requests its (at most four) 16-byte pieces of the batch's x slice (a contiguous
-// 512*nb-wide k range of every token), then the batch's scales, then its weight fragments, all in
-// straight-line code: memory operations complete in order, so the x pieces are written to LDS while the
-// weights are still in flight and each fragment is multiplied as soon as it lands. At M = 1,
-// K = 7168 one batch covers the row group: each wave has all 14 KiB of its weights in flight at once.
-// fp4 is decoded with its scale by V_CVT_SCALEF32_PK_BF16_FP4 and multiplied on
-// V_MFMA_F32_16X16X32_BF16 (tokens are the 16 B columns; columns >= M are zero); the four partial sums
-// meet in LDS.
+// non-gated) [N][K/2], in u8 w_sf (repacked), out bf16 y[M][N], i32 M, launch i32 N, i32 K, i32 nb, i32 sb.
+// Grid N/16, block 256, dynamic LDS M*(sb*1024 + 16) + K/2 bytes: one 16-row group per workgroup. Wave w
+// takes the 128-wide k-tiles kt = 4i + w (equal shares; its scale is byte w of each scale dword of the
+// group). x is consumed in slices of sb k-tiles per wave (sb divides K/512, M*sb <= 16), weights in rounds
+// of nb fragments per wave (nb divides sb). Each slice of x, and with the first slice the row group's
+// whole scale block, goes from memory straight into LDS (buffer loads to LDS, no registers); the round's
+// weight fragments are requested behind them in straight-line code, so waiting for the LDS data leaves
+// the weights in flight, and each fragment is multiplied as soon as it lands. At M = 1, K = 7168 one
+// slice covers the row group and the weights come in two rounds of 7 KiB per wave.
+// fp4 is decoded with its scale by V_CVT_SCALEF32_PK_BF16_FP4 and multiplied on V_MFMA_F32_16X16X32_BF16
+// (tokens are the 16 B columns; columns >= M are computed and dropped); the four partial sums meet in LDS.
+
+// 16 bytes per lane from a buffer straight into LDS at `lds_wave_base + 16 * lane` (wave-uniform base);
+// offsets past the buffer's end read zeros
+KERN_DEV void dma16_buf(__amdgpu_buffer_rsrc_t r, int voffset, void* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_wave_base, 16, voffset, 0, 0, 0);
+}
+
 template <int NB>
 KERN_DEV v4f gemv_rows(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr_, __amdgpu_buffer_rsrc_t sr_, uint16_t* xs,
                        int M, int K, int nk, int sb, int lane, int c, int grp, int wave, bool live) {
   const int row = sb * 512 + 8;  // LDS row stride in bf16 (16 B pad)
-  const int sshift = 8 * wave;
-  const int per_tok = 64 * sb;
-  const int pieces = M * per_tok;  // <= 1024: at most four per lane
-  // token rows >= M read row M of xs, which holds zeros: the B columns of absent tokens are zero
-  const uint16_t* xl = xs + (live ? c : M) * row + wave * 128 + grp * 32;
-  for (int q = threadIdx.x; q < row / 8; q += 256) reinterpret_cast<v4u*>(xs + M * row)[q] = (v4u){0u, 0u, 0u, 0u};
+  const int per_tok = 64 * sb;   // 16-byte pieces of one token's slice: a multiple of 64
+  const int pieces = M * per_tok;         // <= 1024: at most four requests per wave
+  const int spieces = (K >> 9) * 16;      // 16-byte pieces of the row group's scales (<= 512)
+  uint8_t* ss = reinterpret_cast<uint8_t*>(xs + M * row);  // the row group's scales, as stored in HBM
+  // lanes of absent tokens (c >= M) read token 0's row: an MFMA output column depends on its own B
+  // column only, and the columns of absent tokens are never stored
+  const uint16_t* xl = xs + (live ? c : 0) * row + wave * 128 + grp * 32;
+  // this wave's scale byte (k-tile 4*kg + wave) in the dword of this lane at k group kg
+  const uint8_t* sl = ss + lane * 4 + wave;
   const int wv = (wave * 64 + lane) * 16;  // this lane's byte in a 4 KiB group of four fragments
   v4f acc[2] = {};  // two chains, so consecutive MFMAs do not wait on each other
   for (int s0 = 0; s0 < nk; s0 += sb) {
-    // x[:, 512*s0 .. 512*(s0+sb)) in 16-byte pieces q -> token q / per_tok, column (q % per_tok)*8;
-    // lanes past the last piece read beyond the buffer, which returns zeros
-    v4u xv[4];
+    if (s0) __syncthreads();  // every wave's reads of the previous slice are done
+    // x[:, 512*s0 .. 512*(s0+sb)) and (first slice) the scales go from memory straight into LDS:
+    // request r of this wave moves pieces 256r + 64*wave + lane (all of one token: piece q is token
+    // q / per_tok, column (q % per_tok)*8)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int q = (int)threadIdx.x + 256 * r;
-      const int t = q / per_tok, col = (q - t * per_tok) * 8;
-      const int off = q < pieces ? (t * K + s0 * 512 + col) * 2 : 0x7ffffff0;
-      xv[r] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+      const int q0 = 256 * r + 64 * wave;
+      if (q0 < pieces) {
+        const int t = q0 / per_tok, col0 = (q0 - t * per_tok) * 8;
+        dma16_buf(xr, (t * K + s0 * 512 + col0 + lane * 8) * 2, xs + t * row + col0);
+      }
+    }
+    if (s0 == 0) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int q0 = 256 * r + 64 * wave;
+        if (q0 < spieces) dma16_buf(sr_, (q0 + lane) * 16, ss + q0 * 16);
+      }
     }
     for (int i0 = s0; i0 < s0 + sb; i0 += NB) {
-      // scales before weights, so fragment u waits only for itself and the fragments before it; the
+      // weights after x and the scales, so that their wait below leaves the weights in flight; the
       // scheduling barriers keep the issue order as written
-      __builtin_amdgcn_sched_barrier(0);
-      uint32_t sv[NB];
-#pragma unroll
-      for (int u = 0; u < NB; ++u) sv[u] = __builtin_amdgcn_raw_buffer_load_b32(sr_, lane * 4, (i0 + u) * 256, 0);
       __builtin_amdgcn_sched_barrier(0);
       v4u wv4[NB];
 #pragma unroll
@@ -152,18 +176,12 @@ KERN_DEV v4f gemv_rows(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr_, __
         __builtin_amdgcn_sched_barrier(0);
       }
       if (i0 == s0) {
-        if (s0) __syncthreads();  // the previous slice's reads of xs are done
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int q = (int)threadIdx.x + 256 * r;
-          const int t = q / per_tok, col = (q - t * per_tok) * 8;
-          if (q < pieces) *reinterpret_cast<v4u*>(xs + t * row + col) = xv[r];
-        }
-        __syncthreads();
+        WAIT_VMCNT(NB);  // this wave's requests into LDS have landed (only the weights may be in flight)
+        __syncthreads();  // ... and every wave's
       }
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
-        const float s = e8m0_to_f32((sv[u] >> sshift) & 0xffu);
+        const float s = e8m0_to_f32(sl[(i0 + u) * 256]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           // A: 8 fp4 of this lane's row, k = 32*grp + 8*j .. +8 of the tile (dword j of the lane's slot)
@@ -185,9 +203,9 @@ KERN_DEV v4f gemv_rows(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr_, __
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void kern_mx_gemv_bf16(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,
     uint16_t* __restrict__ y, int M, int N, int K, int nb, int sb) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M + 1][sb*512 + 8], row M zero
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][sb*512 + 8], then the scales
   __shared__ v4f red[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rg = blockIdx.x;
   const int KT = K >> 7, KG = K >> 9;
   const int nk = KT >> 2;  // k-tiles of every wave (K % 512 == 0)
@@ -262,8 +280,6 @@ struct BmmArgs {
 #define LDS_SW (16 * 256)
 #define LDS_SX (4 * BT * 4)
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glob_void_t;
 
 // 16 bytes per lane from global memory straight into LDS at `lds_wave_base + 16 * lane` (wave-uniform base)
 KERN_DEV void dma16(const void* g, void* lds_wave_base) {
@@ -273,11 +289,6 @@ KERN_DEV void dma16(const void* g, void* lds_wave_base) {
 KERN_DEV void dma4(const void* g, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((glob_void_t*)g, (lds_void_t*)lds_wave_base, 4, 0, 0);
 }
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
-// lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
-#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | 0x70 | 0xF00 | (((n) >> 4) << 14))
-// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left alone
-#define WAIT_LGKMCNT0 __builtin_amdgcn_s_waitcnt(0xC07F)
 
 // The LDS ring. Each stage and scale slot is its own variable, so that the compiler's wait-count
 // analysis can tell a read of one stage from the loads still landing in another.
