@@ -64,6 +64,9 @@ int kern_module_function(kern_module mod, const char* entry, kern_function* out)
  * Writes up to `cap` sizes; *n gets the count. */
 int kern_function_param_sizes(kern_function fn, uint32_t* sizes, int cap, int* n);
 
+/* Their byte offsets in the kernel-argument segment, from the same metadata. */
+int kern_function_param_offsets(kern_function fn, uint32_t* offsets, int cap, int* n);
+
 /* The same sizes read from a code object image in host memory, without a device (a manifest's
  * launches can be checked against an artifact before any GPU is touched). */
 int kern_code_object_param_sizes(const void* image, size_t len, const char* entry, uint32_t* sizes, int cap,
@@ -85,6 +88,51 @@ int kern_graph_end(void* stream, kern_graph* out);
 int kern_graph_launch(kern_graph g, void* stream);
 int kern_graph_destroy(kern_graph g);
 
+/* Free a handle from kern_module_function (its kernel stays in the module). */
+int kern_function_release(kern_function fn);
+
+/* ------------------------------------------------------------------------------------------------
+ * Manifest-op layer: one kern manifest op, run from its own JSON with its `impl` pointed at a module
+ * loaded here. The op object is the value of one `ops` entry (crates/kern-manifest/src/types.rs:970-1040):
+ * {"params": [...], "impl": {"launches": [{"module", "entry", "params"?, "block", "grid", "shared_mem"?,
+ * "when"?, "args"?}, ...]}}, with grids and shared_mem as Expr trees over manifest vars
+ * (types.rs:1517-1576), args as LaunchArg (types.rs:1174-1191) and packs of Fields (types.rs:1193-1260).
+ * This is the module-swap of candidate::splice (crates/kern-manifest/src/candidate.rs:1-26): the op's
+ * params and every call stay as they are; only `impl` names this module.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct kern_op_s* kern_op;
+
+/* Parse and check an op (the checks of verify.rs:655-700: arg count, forwarded params matching their
+ * launch params in kind and dtype, no writes through `in` params, no reads of `out` params before a
+ * launch wrote them, packs filling exactly their bytes<n>), resolve each launch's entry in `mod`, which
+ * the manifest's `modules` table names `module_name`, and check its params against the code object's
+ * kernel-argument sizes (compile.rs:385-415). Extern launches, scratch buffers, rank args, TMA
+ * descriptors, clusters and programmatic dependent launch have no gfx950 counterpart here:
+ * KERN_ERR_MANIFEST. */
+int kern_op_create(const char* op_json, const char* module_name, kern_module mod, kern_op* out);
+int kern_op_destroy(kern_op op);
+int kern_op_num_params(kern_op op);   /* -1 for a null op */
+int kern_op_num_launches(kern_op op);
+
+/* Run the op's launches in order on `stream` (exec.rs:726-821), each only while its `when` holds.
+ * params[i] is interface param i: a device address for a buffer, otherwise the scalar's bits in the
+ * low bytes (i32 and f32 4, u8 1, i64 8). var_names/var_values bind the manifest vars the grids,
+ * shared_mem, `when` and pack fields read. An unknown var, a grid beyond the launch limits or a failed
+ * launch is KERN_ERR_CALL with the launch's context (compile.rs:725, exec.rs:707). */
+int kern_op_launch(kern_op op, const uint64_t* params, int nparams, const char* const* var_names,
+                   const uint64_t* var_values, int nvars, void* stream);
+
+/* Host-only: what kern_op_launch would do for one launch of an op (no device, no code object), for
+ * checking a manifest against this ABI without a GPU: grid, block, dynamic LDS bytes and the
+ * kernel-argument image (each argument at its natural alignment, bytes<n> aligned to n when n is 1, 2, 4
+ * or 8 and to 8 otherwise, size rounded up to 8; kern_op_launch places arguments at the code object's
+ * own offsets, which agree with this for every entry of kern_mx).
+ * *skip = 1 when the launch's `when` does not hold (nothing else is written then). */
+int kern_op_plan(const char* op_json, int launch_index, const uint64_t* params, int nparams,
+                 const char* const* var_names, const uint64_t* var_values, int nvars, uint32_t grid[3],
+                 uint32_t block[3], uint32_t* shared_bytes, void* kernargs, size_t cap, size_t* kernargs_size,
+                 int* skip);
+
 /* ------------------------------------------------------------------------------------------------
  * Op layer. The library loads its code object kern_mx.hsaco (next to libkern_amd.so unless
  * kern_init names another path) on first use per device and checks the SHA-256 it was built with.
@@ -94,6 +142,9 @@ int kern_graph_destroy(kern_graph g);
 int kern_init(const char* code_object_path);
 /* SHA-256 the library pins its code object to (64 hex chars). */
 const char* kern_code_object_sha256(void);
+/* The library's own module (kern_mx.hsaco, pinned) on the current device, loaded on first use; owned
+ * by the library. This is the module a manifest binds as `kern_mx` for kern_op_create. */
+int kern_mx_module(kern_module* out);
 
 /* moe_quant (fixtures/k3/head.json:25057; rule tools/trtllm-bmm/probe.py:38-43):
  * in bf16 x[T][K], out u8 q[T][K] (e4m3), out u8 sf[T][K/32] (ue8m0, linear), i32 T; launch i32 K.

@@ -49,16 +49,29 @@ int hip_fail(hipError_t e, const char* what) {
 
 }  // namespace
 
+// the same thread-local message, for the other host source files of the library
+int kern_amd_fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
 struct kern_module_s {
   hipModule_t mod = nullptr;
   int device = -1;
-  std::map<std::string, std::vector<uint32_t>> params;  // entry -> explicit arg sizes (code object metadata)
+  std::map<std::string, std::vector<uint32_t>> params;   // entry -> explicit arg sizes (code object metadata)
+  std::map<std::string, std::vector<uint32_t>> offsets;  // entry -> their kernarg byte offsets
 };
 
 struct kern_function_s {
   hipFunction_t fn = nullptr;
   std::string entry;
   std::vector<uint32_t> params;
+  std::vector<uint32_t> offsets;
 };
 
 struct kern_graph_s {
@@ -84,7 +97,7 @@ extern "C" int kern_module_load(const void* image, size_t len, const char* sha25
   }
   std::unique_ptr<kern_module_s> m(new kern_module_s);
   std::string perr;
-  if (!kern::read_kernel_params(static_cast<const uint8_t*>(image), len, m->params, perr))
+  if (!kern::read_kernel_params(static_cast<const uint8_t*>(image), len, m->params, perr, &m->offsets))
     return fail(KERN_ERR_KERNEL_ARTIFACT, "code object metadata: %s", perr.c_str());
   HIP_TRY(hipGetDevice(&m->device), "hipGetDevice");
   HIP_TRY(hipModuleLoadData(&m->mod, image), "hipModuleLoadData");
@@ -108,7 +121,13 @@ extern "C" int kern_module_function(kern_module mod, const char* entry, kern_fun
   HIP_TRY(hipModuleGetFunction(&f->fn, mod->mod, entry), "hipModuleGetFunction");
   f->entry = entry;
   f->params = it->second;
+  f->offsets = mod->offsets[entry];
   *out = f.release();
+  return KERN_OK;
+}
+
+extern "C" int kern_function_release(kern_function fn) {
+  delete fn;  // the hipFunction_t belongs to its module
   return KERN_OK;
 }
 
@@ -116,6 +135,13 @@ extern "C" int kern_function_param_sizes(kern_function fn, uint32_t* sizes, int 
   if (!fn || !n) return fail(KERN_ERR_API, "kern_function_param_sizes: null argument");
   *n = (int)fn->params.size();
   for (int i = 0; i < cap && i < *n; ++i) sizes[i] = fn->params[i];
+  return KERN_OK;
+}
+
+extern "C" int kern_function_param_offsets(kern_function fn, uint32_t* offsets, int cap, int* n) {
+  if (!fn || !n) return fail(KERN_ERR_API, "kern_function_param_offsets: null argument");
+  *n = (int)fn->offsets.size();
+  for (int i = 0; i < cap && i < *n; ++i) offsets[i] = fn->offsets[i];
   return KERN_OK;
 }
 
@@ -181,7 +207,7 @@ extern "C" int kern_graph_end(void* stream, kern_graph* out) {
   if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
   e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
   if (e != hipSuccess) {
-    hipGraphDestroy(g->graph);
+    (void)hipGraphDestroy(g->graph);
     return hip_fail(e, "hipGraphInstantiate");
   }
   *out = g.release();
@@ -196,8 +222,8 @@ extern "C" int kern_graph_launch(kern_graph g, void* stream) {
 
 extern "C" int kern_graph_destroy(kern_graph g) {
   if (!g) return KERN_OK;
-  if (g->exec) hipGraphExecDestroy(g->exec);
-  if (g->graph) hipGraphDestroy(g->graph);
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
   delete g;
   return KERN_OK;
 }
@@ -304,6 +330,11 @@ extern "C" int kern_init(const char* code_object_path) {
 }
 
 extern "C" const char* kern_code_object_sha256(void) { return KERN_MX_SHA256; }
+
+extern "C" int kern_mx_module(kern_module* out) {
+  if (!out) return fail(KERN_ERR_API, "kern_mx_module: null output");
+  return module_for_device(out);
+}
 
 extern "C" int kern_moe_quant(const void* x, void* q, void* sf, int32_t tokens, int32_t K, void* stream) {
   REQUIRE(tokens >= 0 && K > 0 && K % 32 == 0, "moe_quant: need K %% 32 == 0 and tokens >= 0 (K=%d tokens=%d)", K,

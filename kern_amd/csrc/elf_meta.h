@@ -73,8 +73,9 @@ struct MsgPack {
   }
 };
 
-// one kernel map: collect .name and the explicit .args sizes
-inline bool parse_kernel(MsgPack& m, uint64_t nkeys, std::string& name, std::vector<uint32_t>& sizes) {
+// one kernel map: collect .name and the explicit .args sizes and byte offsets
+inline bool parse_kernel(MsgPack& m, uint64_t nkeys, std::string& name, std::vector<uint32_t>& sizes,
+                         std::vector<uint32_t>& offsets) {
   for (uint64_t i = 0; i < nkeys && m.ok; ++i) {
     uint64_t n = 0; int64_t iv = 0; std::string key, val;
     if (m.head(n, iv, key) != 1) return false;
@@ -87,7 +88,7 @@ inline bool parse_kernel(MsgPack& m, uint64_t nkeys, std::string& name, std::vec
       for (uint64_t a = 0; a < na && m.ok; ++a) {
         uint64_t nk = 0;
         if (m.head(nk, iv, val) != 3) return false;
-        int64_t size = -1;
+        int64_t size = -1, offset = -1;
         std::string kind;
         for (uint64_t q = 0; q < nk && m.ok; ++q) {
           std::string k2;
@@ -95,13 +96,19 @@ inline bool parse_kernel(MsgPack& m, uint64_t nkeys, std::string& name, std::vec
           if (k2 == ".size") {
             std::string t;
             m.head(n, size, t);
+          } else if (k2 == ".offset") {
+            std::string t;
+            m.head(n, offset, t);
           } else if (k2 == ".value_kind") {
             if (m.head(n, iv, kind) != 1) return false;
           } else {
             m.skip();
           }
         }
-        if (kind.compare(0, 7, "hidden_") != 0) sizes.push_back((uint32_t)size);
+        if (kind.compare(0, 7, "hidden_") != 0) {
+          sizes.push_back((uint32_t)size);
+          offsets.push_back((uint32_t)offset);
+        }
       }
     } else {
       m.skip();
@@ -111,7 +118,8 @@ inline bool parse_kernel(MsgPack& m, uint64_t nkeys, std::string& name, std::vec
 }
 
 inline bool read_kernel_params(const uint8_t* img, size_t len, std::map<std::string, std::vector<uint32_t>>& out,
-                               std::string& err) {
+                               std::string& err,
+                               std::map<std::string, std::vector<uint32_t>>* offsets_out = nullptr) {
   if (len < 64 || memcmp(img, "\x7f" "ELF", 4) != 0 || img[4] != 2) { err = "not a 64-bit ELF"; return false; }
   uint64_t shoff; uint16_t shentsize, shnum;
   memcpy(&shoff, img + 0x28, 8);
@@ -146,9 +154,10 @@ inline bool read_kernel_params(const uint8_t* img, size_t len, std::map<std::str
             for (uint64_t q = 0; q < nk; ++q) {
               uint64_t nkeys = 0;
               if (m.head(nkeys, iv, t) != 3) { err = "kernel entry is not a map"; return false; }
-              std::string name; std::vector<uint32_t> sizes;
-              if (!parse_kernel(m, nkeys, name, sizes)) { err = "malformed kernel entry"; return false; }
+              std::string name; std::vector<uint32_t> sizes, offsets;
+              if (!parse_kernel(m, nkeys, name, sizes, offsets)) { err = "malformed kernel entry"; return false; }
               out[name] = sizes;
+              if (offsets_out) (*offsets_out)[name] = offsets;
             }
           } else {
             m.skip();

@@ -1,0 +1,141 @@
+"""Manifest ops of the MXFP4 matmul path with their `impl` pointed at this build's gfx950 module.
+
+Each function returns one `ops` entry of a kern manifest (crates/kern-manifest/src/types.rs:970-1040):
+the op's interface `params`, kept exactly as the reference declares them
+(crates/kern-manifest/tests/fixtures/k3/head.json: moe_quant :25057, k3_moe_w_shuffle :26358,
+k3_moe_sf_shuffle :26413, moe_routing :25117, moe_fc1 :25459, moe_fc2 :25683), and an `impl` whose
+launches name module `kern_mx` (kernel_index/kern_mx.toml). Swapping a manifest's `impl` for these is
+the module swap of candidate::splice (crates/kern-manifest/src/candidate.rs:1-26): calls and params do
+not change. Shape constants a launch needs (hidden size, expert count, top-k) are literals of the launch,
+as in the reference's own launches; `tokens` is the manifest var the grids read.
+
+The grammar is the reference's: grids are Expr trees (types.rs:1517-1576), args LaunchArg
+(types.rs:1174-1191). A launch arg cannot name a var directly, so the one kernel argument that is the
+var `tokens` (moe_routing's token count) travels as a 4-byte pack, the form the reference uses for
+struct-taking kernels (types.rs:1193-1260).
+"""
+from __future__ import annotations
+
+MODULE = "kern_mx"
+BMM_THREADS = 512  # threads of one GEMM workgroup (8 waves)
+
+
+def _ceil(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def moe_quant(K: int) -> dict:
+    """moe_quant(in bf16 x[T][K], out u8 q[T][K], out u8 sf[T][K/32], i32 T); launch adds i32 K.
+    A 256-thread workgroup covers 512 chunks of 8 elements: grid ceil(T*K/8 / 512)."""
+    assert K % 32 == 0
+    return {
+        "params": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32"],
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_quant_bf16",
+            "params": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "i32"],
+            "block": [256, 1, 1],
+            "grid": [{"ceil_div": [{"mul": ["tokens", K // 8]}, 512]}, 1, 1],
+            "args": [{"param": 0}, {"param": 1}, {"param": 2}, {"param": 3}, {"i32": K}],
+        }]},
+    }
+
+
+def k3_moe_w_shuffle(E: int, max_bytes: int) -> dict:
+    """k3_moe_w_shuffle(in u8 raw, out u8 repacked, i32 rows, i32 row_bytes, i32 gated); launch prepends
+    i32 E after the buffers. The grid covers the largest call, max_bytes = rows*row_bytes per expert (the
+    kernel bounds-checks smaller ones), as the reference's fixed grid does."""
+    return {
+        "params": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32"],
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_w_shuffle",
+            "params": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
+            "block": [256, 1, 1],
+            "grid": [_ceil(E * max_bytes // 16, 256), 1, 1],
+            "args": [{"param": 0}, {"param": 1}, {"i32": E}, {"param": 2}, {"param": 3}, {"param": 4}],
+        }]},
+    }
+
+
+def k3_moe_sf_shuffle(E: int, max_bytes: int) -> dict:
+    """k3_moe_sf_shuffle(in u8 raw, out u8 repacked, i32 rows, i32 sf_cols, i32 gated); launch prepends i32 E.
+    The grid covers the largest call, max_bytes = rows*sf_cols per expert."""
+    return {
+        "params": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32"],
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_sf_shuffle",
+            "params": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
+            "block": [256, 1, 1],
+            "grid": [_ceil(E * max_bytes // 4, 256), 1, 1],
+            "args": [{"param": 0}, {"param": 1}, {"i32": E}, {"param": 2}, {"param": 3}, {"param": 4}],
+        }]},
+    }
+
+
+def moe_routing(topk: int, local_start: int, local_experts: int) -> dict:
+    """moe_routing(in i32 topk_idx, out i32 counts, cta_batch, cta_limit, num_non_exiting, total_padded,
+    route_map, exp2perm); launch adds the token count (var `tokens`), top-k and the local expert range."""
+    bufs = ["in buffer<i32>"] + ["out buffer<i32>"] * 7
+    return {
+        "params": bufs,
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_routing",
+            "params": bufs + ["bytes<4>", "i32", "i32", "i32"],
+            "block": [1024, 1, 1],
+            "grid": [1, 1, 1],
+            "args": [{"param": i} for i in range(8)]
+            + [{"pack": {"size": 4, "fields": [{"at": 0, "var": "tokens"}]}},
+               {"i32": topk}, {"i32": local_start}, {"i32": local_experts}],
+        }]},
+    }
+
+
+def _slots(topk: int, experts: int) -> dict:
+    # grid.y: the reference's CTA-slot bound E + ceil(tokens*topk/128) (tools/kernels/abi/trtllm_bmm.py:58-60)
+    return {"add": [{"ceil_div": [{"mul": ["tokens", topk]}, 128]}, experts]}
+
+
+def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
+    """moe_fc1 = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (13 params); launch adds i32 m (= 2I), i32 k (= H) and a
+    null f32 debug pointer (an i64 zero)."""
+    assert m % 256 == 0 and k % 512 == 0
+    p = ["in buffer<u8>"] * 4 + ["out buffer<u8>"] * 2 + ["in buffer<i32>", "in buffer<f32>", "in buffer<f32>"] \
+        + ["in buffer<i32>"] * 4
+    return {
+        "params": p,
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_bmm_fc1",
+            "params": p + ["i32", "i32", "i64"],
+            "block": [BMM_THREADS, 1, 1],
+            "grid": [m // 256, _slots(topk, experts), 1],
+            "args": [{"param": i} for i in range(13)] + [{"i32": m}, {"i32": k}, {"i64": 0}],
+        }]},
+    }
+
+
+def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
+    """moe_fc2 = trtllm_bmm_bf16_mxe2m1_mxe4m3 (9 params); launch adds i32 m (= H), i32 k (= I),
+    i32 sf_b_r128c4 = 1 (FC1 writes its scales R128c4) and a null f32 debug pointer."""
+    assert m % 256 == 0 and k % 512 == 0
+    p = ["in buffer<u8>"] * 4 + ["out buffer<bf16>"] + ["in buffer<i32>"] * 4
+    return {
+        "params": p,
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_bmm_fc2",
+            "params": p + ["i32", "i32", "i32", "i64"],
+            "block": [BMM_THREADS, 1, 1],
+            "grid": [m // 256, _slots(topk, experts), 1],
+            "args": [{"param": i} for i in range(9)] + [{"i32": m}, {"i32": k}, {"i32": 1}, {"i64": 0}],
+        }]},
+    }
+
+
+def moe_ops(H: int, I: int, E: int, topk: int, local_start: int = 0) -> dict:
+    """The six ops of one MoE layer (hidden H, intermediate I, E local experts, top-k) as `ops` entries."""
+    return {
+        "moe_quant": moe_quant(H),
+        "k3_moe_w_shuffle": k3_moe_w_shuffle(E, max(2 * I * H // 2, H * I // 2)),
+        "k3_moe_sf_shuffle": k3_moe_sf_shuffle(E, max(2 * I * H // 32, H * I // 32)),
+        "moe_routing": moe_routing(topk, local_start, E),
+        "moe_fc1": moe_fc1(2 * I, H, E, topk),
+        "moe_fc2": moe_fc2(H, I, E, topk),
+    }

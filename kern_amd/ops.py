@@ -11,7 +11,9 @@ fallback: without the built library every call raises.
 from __future__ import annotations
 
 import ctypes
+import json
 import os
+import struct
 
 import torch
 
@@ -59,6 +61,16 @@ _SIGS = {
     "kern_graph_end": [P, P],
     "kern_graph_launch": [P, P],
     "kern_graph_destroy": [P],
+    "kern_function_release": [P],
+    "kern_function_param_offsets": [P, P, ctypes.c_int, P],
+    "kern_mx_module": [P],
+    "kern_op_create": [ctypes.c_char_p, ctypes.c_char_p, P, P],
+    "kern_op_destroy": [P],
+    "kern_op_num_params": [P],
+    "kern_op_num_launches": [P],
+    "kern_op_launch": [P, P, ctypes.c_int, P, P, ctypes.c_int, P],
+    "kern_op_plan": [ctypes.c_char_p, ctypes.c_int, P, ctypes.c_int, P, P, ctypes.c_int, P, P, P, P, ctypes.c_size_t,
+                     P, P],
 }
 
 
@@ -227,3 +239,91 @@ def repack_weights(raw_w: torch.Tensor, raw_sf: torch.Tensor, gated: bool = Fals
     k3_moe_w_shuffle(raw_w, w, rows, rb, gated, experts=E)
     k3_moe_sf_shuffle(raw_sf, sf, rows, raw_sf.shape[2], gated, experts=E)
     return w, sf
+
+
+# ------------------------------------------------------------------------------- manifest ops
+
+def _op_params(op: dict, params) -> ctypes.Array:
+    """Interface params as the C ABI takes them: device addresses for buffers, scalar bits otherwise."""
+    types = op["params"]
+    if len(params) != len(types):
+        raise KernError(4, f"the op takes {len(types)} params, got {len(params)}")
+    vals = (ctypes.c_uint64 * max(1, len(types)))()
+    for i, (t, v) in enumerate(zip(types, params)):
+        if t is None:
+            vals[i] = int(v)
+        elif "buffer<" in t:
+            vals[i] = v.data_ptr() if isinstance(v, torch.Tensor) else int(v)
+        elif t == "f32":
+            vals[i] = struct.unpack("<I", struct.pack("<f", float(v)))[0]
+        elif t == "i64":
+            vals[i] = int(v) & (2**64 - 1)
+        elif t == "u8":
+            vals[i] = int(v) & 0xFF
+        else:
+            vals[i] = int(v) & 0xFFFFFFFF
+    return vals
+
+
+def _vars(vars_: dict | None):
+    vars_ = vars_ or {}
+    names = (ctypes.c_char_p * max(1, len(vars_)))(*[k.encode() for k in vars_])
+    values = (ctypes.c_uint64 * max(1, len(vars_)))(*[int(v) for v in vars_.values()])
+    return names, values, len(vars_)
+
+
+class ManifestOp:
+    """One kern manifest op (an `ops` entry: params + impl.launches) run through kern_op_* with its
+    launches bound to this library's own module, which the manifest names `module_name`
+    (crates/kern-manifest/src/candidate.rs:1-26 swaps an op's impl the same way)."""
+
+    def __init__(self, op: dict | str, module_name: str = "kern_mx"):
+        self.op = json.loads(op) if isinstance(op, str) else op
+        mod = ctypes.c_void_p()
+        check(lib().kern_mx_module(ctypes.byref(mod)))
+        h = ctypes.c_void_p()
+        check(lib().kern_op_create(json.dumps(self.op).encode(), module_name.encode(), mod, ctypes.byref(h)))
+        self._h = h
+        self.num_launches = lib().kern_op_num_launches(h)
+
+    def __call__(self, *params, vars: dict | None = None):
+        """Run the op's launches on torch's current stream; `vars` binds the manifest vars (e.g. tokens)."""
+        vals = _op_params(self.op, params)
+        names, values, n = _vars(vars)
+        check(lib().kern_op_launch(self._h, ctypes.cast(vals, P), len(params), ctypes.cast(names, P),
+                                   ctypes.cast(values, P), n, _stream()))
+
+    def close(self):
+        if self._h:
+            lib().kern_op_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def op_plan(op: dict | str, launch: int, params, vars: dict | None = None) -> dict:
+    """Host-only plan of one launch of a manifest op (no device): grid, block, dynamic LDS bytes and
+    the kernel-argument image; skip is True when the launch's `when` does not hold."""
+    if isinstance(op, str):
+        text = op
+        try:  # the param types; malformed text goes to the library as it is, which reports it
+            types = {"params": json.loads(op).get("params", [])}
+        except (ValueError, AttributeError):
+            types = {"params": [None] * len(params)}
+    else:
+        text, types = json.dumps(op), op
+    vals = _op_params(types, params)
+    names, values, n = _vars(vars)
+    grid, block = (ctypes.c_uint32 * 3)(), (ctypes.c_uint32 * 3)()
+    shared, size, skip = ctypes.c_uint32(), ctypes.c_size_t(), ctypes.c_int()
+    buf = (ctypes.c_uint8 * 4096)()
+    check(lib().kern_op_plan(text.encode(), launch, ctypes.cast(vals, P), len(params),
+                             ctypes.cast(names, P), ctypes.cast(values, P), n, ctypes.cast(grid, P),
+                             ctypes.cast(block, P), ctypes.byref(shared), ctypes.cast(buf, P), 4096,
+                             ctypes.byref(size), ctypes.byref(skip)))
+    return {"grid": tuple(grid), "block": tuple(block), "shared": shared.value,
+            "args": bytes(buf[:size.value]) if not skip.value else b"", "skip": bool(skip.value)}

@@ -1,0 +1,119 @@
+"""Manifest-op layer on the GPU: the path's ops, run from their manifest JSON through kern_op_create /
+kern_op_launch with impl pointed at kern_mx, give bit-identical results to the direct C-ABI entry
+points (same kernels, same arguments); create-time checks against the code object reject mismatches."""
+import numpy as np
+import pytest
+import torch
+
+from kern_amd import manifest as mf
+from kern_amd import workload as wl
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from kern_amd import ops as o
+    o.lib()
+    return o
+
+
+def _dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(a).cuda()
+
+
+def _r128c4_bytes(rows, blocks):
+    return (rows // 128) * 512 * -(-blocks // 4)
+
+
+def test_moe_layer_through_manifest_ops(ops):
+    T, E, k, H, I = 64, 8, 2, 1024, 512
+    print(f"[manifest] MoE layer T={T} E={E} k={k} H={H} I={I}", flush=True)
+    man = {n: ops.ManifestOp(o) for n, o in mf.moe_ops(H, I, E, k).items()}
+    v = {"tokens": T}
+    x = _dev(wl.activations_bf16(71, T, H))
+    ids = _dev(wl.topk_ids(72, T, E, k))
+    w13, s13 = (_dev(a) for a in wl.mxfp4_weights(73, E, 2 * I, H, 119, 124))
+    w2, s2 = (_dev(a) for a in wl.mxfp4_weights(74, E, H, I, 119, 124))
+    alpha = torch.full((E,), 4.0, device="cuda")
+    beta = torch.full((E,), 25.0, device="cuda")
+    ctas = ops.ctas_bound(T, k, E)
+    rows = ctas * 128
+    u8, i32 = torch.uint8, torch.int32
+
+    def run(manifest: bool):
+        out = {"q": torch.zeros((T, H), dtype=u8, device="cuda"), "qs": torch.zeros((T, H // 32), dtype=u8, device="cuda"),
+               "w13": torch.zeros_like(w13), "s13": torch.zeros_like(s13), "w2": torch.zeros_like(w2),
+               "s2": torch.zeros_like(s2)}
+        tabs = [torch.full((n,), -7, dtype=i32, device="cuda") for n in (2 * E, ctas, ctas, 1, 1, rows, T * k)]
+        c1 = torch.zeros((rows, I), dtype=u8, device="cuda")
+        sf1 = torch.zeros(_r128c4_bytes(rows, I // 32), dtype=u8, device="cuda")
+        c2 = torch.zeros((rows, H), dtype=torch.bfloat16, device="cuda")
+        counts, cb, cl, nne, tp, rmap, e2p = tabs
+        if manifest:
+            man["moe_quant"](x, out["q"], out["qs"], T, vars=v)
+            man["k3_moe_w_shuffle"](w13, out["w13"], 2 * I, H // 2, 1, vars=v)
+            man["k3_moe_sf_shuffle"](s13, out["s13"], 2 * I, H // 32, 1, vars=v)
+            man["k3_moe_w_shuffle"](w2, out["w2"], H, I // 2, 0, vars=v)
+            man["k3_moe_sf_shuffle"](s2, out["s2"], H, I // 32, 0, vars=v)
+            man["moe_routing"](ids, counts, cb, cl, nne, tp, rmap, e2p, vars=v)
+            man["moe_fc1"](out["w13"], out["s13"], out["q"], out["qs"], c1, sf1, rmap, alpha, beta, nne, tp, cb, cl,
+                           vars=v)
+            man["moe_fc2"](out["w2"], out["s2"], c1, sf1, c2, nne, tp, cb, cl, vars=v)
+        else:
+            ops.moe_quant(x, out["q"], out["qs"], T, K=H)
+            ops.k3_moe_w_shuffle(w13, out["w13"], 2 * I, H // 2, True, experts=E)
+            ops.k3_moe_sf_shuffle(s13, out["s13"], 2 * I, H // 32, True, experts=E)
+            ops.k3_moe_w_shuffle(w2, out["w2"], H, I // 2, False, experts=E)
+            ops.k3_moe_sf_shuffle(s2, out["s2"], H, I // 32, False, experts=E)
+            ops.moe_routing(ids, counts, cb, cl, nne, tp, rmap, e2p, tokens=T, topk=k, local_start=0, local_experts=E)
+            ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(out["w13"], out["s13"], out["q"], out["qs"], c1, sf1, rmap, alpha, beta,
+                                                nne, tp, cb, cl, m=2 * I, k=H, ctas=ctas)
+            ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(out["w2"], out["s2"], c1, sf1, c2, nne, tp, cb, cl, m=H, k=I, ctas=ctas)
+        torch.cuda.synchronize()
+        out.update({f"tab{i}": t for i, t in enumerate(tabs)})
+        out.update({"c1": c1, "sf1": sf1, "c2": c2})
+        return out
+
+    a, b = run(False), run(True)
+    assert int(a["tab3"][0]) > 0
+    for name in a:
+        assert torch.equal(a[name].view(torch.uint8) if a[name].dtype == torch.bfloat16 else a[name],
+                           b[name].view(torch.uint8) if b[name].dtype == torch.bfloat16 else b[name]), name
+
+
+def test_create_checks_against_code_object(ops):
+    o = mf.moe_fc2(1024, 512, 8, 2)
+    with pytest.raises(ops.KernError) as e:  # the manifest names another module
+        ops.ManifestOp(o, module_name="other")
+    assert e.value.code == 1
+    bad = mf.moe_fc2(1024, 512, 8, 2)
+    launch = bad["impl"]["launches"][0]
+    launch["params"] = launch["params"][:-2] + ["i64"]  # drop one i32: the code object disagrees
+    launch["args"] = launch["args"][:-2] + [{"i64": 0}]
+    with pytest.raises(ops.KernError) as e:
+        ops.ManifestOp(bad)
+    assert e.value.code == 2 and "code object has" in str(e.value)
+    bad = mf.moe_fc2(1024, 512, 8, 2)
+    bad["impl"]["launches"][0]["entry"] = "kern_mx_no_such_entry"
+    with pytest.raises(ops.KernError) as e:
+        ops.ManifestOp(bad)
+    assert e.value.code == 2
+
+
+def test_launch_errors_carry_context(ops):
+    m = ops.ManifestOp(mf.moe_quant(1024))
+    x = torch.zeros((4, 1024), dtype=torch.bfloat16, device="cuda")
+    q = torch.zeros((4, 1024), dtype=torch.uint8, device="cuda")
+    s = torch.zeros((4, 32), dtype=torch.uint8, device="cuda")
+    with pytest.raises(ops.KernError) as e:
+        m(x, q, s, 4)  # no `tokens` bound
+    assert e.value.code == 7 and "launch #0" in str(e.value)
+    with pytest.raises(ops.KernError) as e:
+        m(x, q, 0, 4, vars={"tokens": 4})  # a null buffer
+    assert e.value.code == 4

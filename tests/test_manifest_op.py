@@ -1,0 +1,196 @@
+"""Manifest-op layer of the C ABI (kern_op_*), host side: no device is touched.
+
+The ops come from kern_amd.manifest (the path's six ops with their impl pointed at kern_mx). Their
+interface params are pinned to the reference's K3 manifest (tests/golden/k3_op_interfaces.json, taken
+from crates/kern-manifest/tests/fixtures/k3/head.json by tests/golden/make_k3_interfaces.py). Grid
+expressions are checked against their closed forms (crates/kern-manifest/src/types.rs:1517-1576) and the
+kernel-argument images against an independent packing of the AMDGPU layout.
+"""
+import json
+import os
+import struct
+
+import pytest
+
+from kern_amd import manifest as mf
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ops = pytest.importorskip("kern_amd.ops")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(ops.LIB_PATH):
+        pytest.skip("library not built")
+    return ops.lib()
+
+
+def golden():
+    with open(os.path.join(HERE, "golden", "k3_op_interfaces.json")) as f:
+        return json.load(f)["ops"]
+
+
+def pack(fields):
+    """AMDGPU kernel-argument image: (format, value) pairs, each at its natural alignment, padded to 8."""
+    out = b""
+    for fmt, v in fields:
+        size = struct.calcsize("<" + fmt)
+        out += b"\0" * (-len(out) % size)
+        out += struct.pack("<" + fmt, v)
+    return out + b"\0" * (-len(out) % 8)
+
+
+# K3 (the reference's own shapes) and BASELINE config 4
+SHAPES = [dict(H=3584, I=3072, E=224, k=16), dict(H=7168, I=2048, E=256, k=8)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_interfaces_match_reference(shape):
+    g = golden()
+    o = mf.moe_ops(shape["H"], shape["I"], shape["E"], shape["k"])
+    for name, rec in g.items():
+        assert o[name]["params"] == rec["params"], name
+
+
+def test_k3_grids_match_reference():
+    g = golden()
+    o = mf.moe_ops(3584, 3072, 224, 16)
+    # the weight repack: one thread per 16-byte slot, as the reference's fixed grid
+    assert o["k3_moe_w_shuffle"]["impl"]["launches"][0]["grid"] == g["k3_moe_w_shuffle"]["grid"]
+    # the CTA-slot axis of both GEMMs is the reference's expression, verbatim
+    for name in ("moe_fc1", "moe_fc2"):
+        assert o[name]["impl"]["launches"][0]["grid"][1] == g[name]["grid"][1], name
+
+
+@pytest.mark.parametrize("T", [1, 37, 512, 8192])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_plan_grids_and_kernargs(lib, shape, T):
+    H, I, E, k = shape["H"], shape["I"], shape["E"], shape["k"]
+    o = mf.moe_ops(H, I, E, k)
+    v = {"tokens": T}
+    slots = E + -(-T * k // 128)
+    bufs = lambda n: [0x1000 * (i + 1) for i in range(n)]
+
+    p = ops.op_plan(o["moe_quant"], 0, bufs(3) + [T], v)
+    assert p["grid"] == (-(-T * H // 8 // 512), 1, 1) and p["block"] == (256, 1, 1)
+    assert p["args"] == pack([("Q", 0x1000), ("Q", 0x2000), ("Q", 0x3000), ("i", T), ("i", H)])
+
+    p = ops.op_plan(o["moe_routing"], 0, bufs(8), v)
+    assert p["grid"] == (1, 1, 1) and p["block"] == (1024, 1, 1)
+    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(8)] + [("i", T), ("i", k), ("i", 0), ("i", E)])
+
+    p = ops.op_plan(o["moe_fc1"], 0, bufs(13), v)
+    assert p["grid"] == (2 * I // 256, slots, 1) and p["block"] == (512, 1, 1)
+    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(13)] + [("i", 2 * I), ("i", H), ("q", 0)])
+
+    p = ops.op_plan(o["moe_fc2"], 0, bufs(9), v)
+    assert p["grid"] == (H // 256, slots, 1)
+    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(9)] + [("i", H), ("i", I), ("i", 1), ("q", 0)])
+
+    for name, rows, rb, gated in [("k3_moe_w_shuffle", 2 * I, H // 2, 1), ("k3_moe_sf_shuffle", H, I // 32, 0)]:
+        p = ops.op_plan(o[name], 0, bufs(2) + [rows, rb, gated], v)
+        assert p["args"] == pack([("Q", 0x1000), ("Q", 0x2000), ("i", E), ("i", rows), ("i", rb), ("i", gated)])
+
+
+def _probe(grid_x, when=None, args=None, params=None, extra=None):
+    launch = {"module": "kern_mx", "entry": "e", "params": params or ["i32"], "block": [64, 1, 1],
+              "grid": [grid_x, 1, 1], "args": args if args is not None else [{"i32": 7}]}
+    if when:
+        launch["when"] = when
+    launch.update(extra or {})
+    return {"params": [], "impl": {"launches": [launch]}}
+
+
+@pytest.mark.parametrize("tokens", [0, 1, 127, 128, 129, 4096, 5000, 8192, 9000])
+def test_expr_closed_forms(lib, tokens):
+    # Expr::eval (types.rs:1560-1576): ceil_div, mul, add, clamp(e, start, len) = min(max(e - start, 0), len)
+    cases = [({"ceil_div": ["tokens", 128]}, -(-tokens // 128)),
+             ({"mul": ["tokens", 16]}, tokens * 16),
+             ({"add": [{"ceil_div": [{"mul": ["tokens", 16]}, 128]}, 224]}, 224 + -(-tokens * 16 // 128)),
+             ({"clamp": ["tokens", 4096, 4096]}, min(max(tokens - 4096, 0), 4096)),
+             (5, 5)]
+    for expr, want in cases:
+        p = ops.op_plan(_probe(expr), 0, [], {"tokens": tokens})
+        assert p["grid"][0] == want, expr
+
+
+@pytest.mark.parametrize("tokens,skip", [(3, True), (4, False), (16, False), (17, True)])
+def test_when_range(lib, tokens, skip):
+    p = ops.op_plan(_probe(1, when={"var": "tokens", "min": 4, "max": 16}), 0, [], {"tokens": tokens})
+    assert p["skip"] is skip
+
+
+def test_pack_fields_and_scalars(lib):
+    op = {"params": ["in buffer<f32>", "f32", "i64", "u8"],
+          "impl": {"launches": [{"module": "kern_mx", "entry": "e",
+                                 "params": ["bytes<24>", "f32", "i64", "u8", "f32"], "block": [64, 1, 1],
+                                 "grid": [1, 1, 1],
+                                 "args": [{"pack": {"size": 24, "fields": [
+                                     {"at": 0, "param": 0}, {"at": 8, "var": "tokens"},
+                                     {"at": 12, "expr": {"mul": ["tokens", 3]}}, {"at": 16, "i64": -2},
+                                 ]}}, {"param": 1}, {"param": 2}, {"param": 3}, {"f32": 0.5}]}]}}
+    p = ops.op_plan(op, 0, [0xABCDEF00, 1.25, -5, 200], {"tokens": 11})
+    img = struct.pack("<QIIq", 0xABCDEF00, 11, 33, -2)  # bytes<24>, aligned to 8
+    img += struct.pack("<f", 1.25) + b"\0" * 4 + struct.pack("<q", -5) + struct.pack("<B", 200)
+    img += b"\0" * 3 + struct.pack("<f", 0.5)
+    img += b"\0" * (-len(img) % 8)
+    assert p["args"] == img
+
+
+BAD = [
+    ("not json", "{", 1),
+    ("extern launch", {"params": [], "impl": {"launches": [{"entry": "extern:cublaslt_bf16_tn", "block": [1, 1, 1],
+                                                             "grid": [1, 1, 1]}]}}, 1),
+    ("cluster", _probe(1, extra={"cluster": [2, 1, 1]}), 1),
+    ("pdl", _probe(1, extra={"pdl": True}), 1),
+    ("unknown key", _probe(1, extra={"stream": 3}), 1),
+    ("block too big", _probe(1, extra={"block": [1024, 2, 1]}), 1),
+    ("arg count", _probe(1, args=[]), 1),
+    ("literal kind", _probe(1, args=[{"i64": 3}]), 1),
+    ("scratch", _probe(1, params=["in buffer<u8>"], args=[{"scratch": "s"}]), 1),
+    ("tensormap", _probe(1, params=["bytes<128>"], args=[{"pack": {"size": 128, "fields": [
+        {"at": 0, "tensormap": {"param": 0}}]}}]), 1),
+    ("pack overflow", _probe(1, params=["bytes<8>"], args=[{"pack": {"size": 8, "fields": [
+        {"at": 4, "i64": 1}]}}]), 1),
+    ("pack size", _probe(1, params=["bytes<8>"], args=[{"pack": {"size": 16, "fields": []}}]), 1),
+    ("bad expr", _probe({"div": ["tokens", 2]}), 1),
+]
+
+
+@pytest.mark.parametrize("name,op,code", BAD, ids=[b[0] for b in BAD])
+def test_malformed_ops_rejected(lib, name, op, code):
+    with pytest.raises(ops.KernError) as e:
+        ops.op_plan(op, 0, [], {"tokens": 1})
+    assert e.value.code == code, str(e.value)
+
+
+def test_dtype_and_direction_checks(lib):
+    base = {"params": ["in buffer<u8>", "out buffer<bf16>"],
+            "impl": {"launches": [{"module": "kern_mx", "entry": "e", "block": [64, 1, 1], "grid": [1, 1, 1],
+                                   "params": ["in buffer<u8>", "out buffer<bf16>"],
+                                   "args": [{"param": 0}, {"param": 1}]}]}}
+    ops.op_plan(base, 0, [1, 2], {})  # consistent
+    bad_dtype = json.loads(json.dumps(base))
+    bad_dtype["impl"]["launches"][0]["params"][1] = "out buffer<f32>"
+    bad_write = json.loads(json.dumps(base))
+    bad_write["impl"]["launches"][0]["params"][0] = "out buffer<u8>"
+    bad_read = json.loads(json.dumps(base))
+    bad_read["impl"]["launches"][0]["params"][1] = "in buffer<bf16>"
+    for op, msg in [(bad_dtype, "does not match"), (bad_write, "writes through interface `in`"),
+                    (bad_read, "read before any launch wrote it")]:
+        with pytest.raises(ops.KernError) as e:
+            ops.op_plan(op, 0, [1, 2], {})
+        assert e.value.code == 1 and msg in str(e.value)
+
+
+def test_call_errors(lib):
+    o = mf.moe_ops(7168, 2048, 256, 8)
+    with pytest.raises(ops.KernError) as e:  # a grid var that is not bound
+        ops.op_plan(o["moe_fc2"], 0, [1] * 9, {})
+    assert e.value.code == 7 and "unknown var `tokens`" in str(e.value)
+    with pytest.raises(ops.KernError) as e:  # wrong number of interface params
+        ops.op_plan(o["moe_fc2"], 0, [1] * 8, {"tokens": 1})
+    assert e.value.code == 4
+    with pytest.raises(ops.KernError) as e:  # grid.y beyond the launch limit
+        ops.op_plan(o["moe_fc2"], 0, [1] * 9, {"tokens": 1 << 20})
+    assert e.value.code == 7 and "exceeds the launch limit" in str(e.value)
