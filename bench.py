@@ -1,6 +1,6 @@
 """Benchmark of the MXFP4 matmul path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemm|decode|moe|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemm|decode|moe|stack|copy]
 
 Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
 
@@ -22,6 +22,12 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
   with ~6 GB of repacked weights (every expert is hit), so each step streams its weights from HBM; GB/s of
   algorithmic bytes (weights of the experts hit + routed activations in and out) against the HBM peak,
   for the step and for FC1 and FC2 alone.
+* `stack` = config 5: four layers of (QKV [M,7168]x[9216,7168], O [M,8192]x[7168,8192], MoE as config 4)
+  at M = 1, 64, 2048, each program captured once through the library's own hipGraph C ABI
+  (kern_graph_begin/end) and replayed. M <= 16 takes the decode GEMV for QKV and O, larger M quantizes
+  to MXFP8 and takes the GEMM; the O input stands in for attention (out of scope) and each layer's O
+  output feeds the next layer. Reported per M: step time, algorithmic HBM bytes (weights touched +
+  activations) as GB/s and FLOPs as TFLOP/s.
 * `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on a bounded
   sample of the same GEMM (its first rows), in the headline unit.
 * `traffic` comes from committed rocprofv3 --pmc summaries (profiles/traffic.json), null without one.
@@ -49,6 +55,8 @@ PM, PN, PK = 4096, 2048, 7168
 DN, DK = 18432, 7168
 # config 4 (MoE grouped)
 MT, ME, MTOP, MH, MI = 512, 256, 8, 7168, 2048
+# config 5 (layer stack)
+S_LAYERS, S_QKV, S_OIN, S_MS = 4, 9216, 8192, (1, 64, 2048)
 MALL_BYTES = 256 << 20
 
 
@@ -58,7 +66,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["gemm", "decode", "moe", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "decode", "moe", "stack", "copy"], default=None,
                     help="run one leg only (for profiling); the JSON line then carries that leg. 'copy' runs "
                          "three plain 256 MiB device copies: the reference for scaling HBM byte counters")
     ap.add_argument("--decode-m", type=int, default=1)
@@ -253,6 +261,114 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
             "bytes_fc1": b_fc1, "bytes_fc2": b_fc2, "bytes_step": b_step, "experts_hit": hit, "slots": ctas}
 
 
+def bench_stack(torch, ops, wl, stream, steps, warmup):
+    """Config 5: the layer stack at each M, one hipGraph per M captured through kern_graph_*."""
+    u8, i32, bf16 = torch.uint8, torch.int32, torch.bfloat16
+    H, I, E, k = MH, MI, ME, MTOP
+    log(f"config 5: {S_LAYERS} layers, generating weights")
+
+    def dense(seed, n, kk):
+        w_raw = torch.empty((n, kk // 2), dtype=u8, device="cuda")
+        s_raw = torch.empty((n, kk // 32), dtype=u8, device="cuda")
+        ops.fill_random_u8(w_raw, wl.tensor_seed(seed, 3))
+        ops.fill_random_u8(s_raw, wl.tensor_seed(seed, 4), 119, 6)
+        out = ops.repack_weights(w_raw, s_raw)
+        del w_raw, s_raw
+        return out
+
+    def experts(seed, rows, kk, gated):
+        w_raw = torch.empty((E, rows, kk // 2), dtype=u8, device="cuda")
+        s_raw = torch.empty((E, rows, kk // 32), dtype=u8, device="cuda")
+        ops.fill_random_u8(w_raw, wl.tensor_seed(seed, 3))
+        ops.fill_random_u8(s_raw, wl.tensor_seed(seed, 4), 119, 6)
+        out = ops.repack_weights(w_raw, s_raw, gated=gated)
+        del w_raw, s_raw
+        return out
+
+    layers = []
+    for l in range(S_LAYERS):
+        layers.append({"qkv": dense(500 + l, S_QKV, H), "o": dense(510 + l, H, S_OIN),
+                       "w13": experts(520 + l, 2 * I, H, True), "w2": experts(530 + l, H, I, False)})
+        torch.cuda.synchronize()
+    alpha = torch.full((E,), 4.0, dtype=torch.float32, device="cuda")
+    beta = torch.full((E,), 25.0, dtype=torch.float32, device="cuda")
+    per_expert = 2 * I * H * 17 // 32 + H * I * 17 // 32
+    w_dense = S_QKV * H * 17 // 32 + H * S_OIN * 17 // 32
+    res = {}
+    for M in S_MS:
+        ids_np = [wl.topk_ids(540 + l + 10 * M, M, E, k) for l in range(S_LAYERS)]
+        ids = [torch.from_numpy(a).cuda() for a in ids_np]
+        x0 = dev_from_np(wl.activations_bf16(550 + M, M, H), torch)
+        attn = dev_from_np(wl.activations_bf16(551 + M, M, S_OIN), torch)
+        ctas = ops.ctas_bound(M, k, E)
+        rows = ctas * 128
+        qkv = torch.empty((M, S_QKV), dtype=bf16, device="cuda")
+        o = [torch.empty((M, H), dtype=bf16, device="cuda") for _ in range(S_LAYERS)]
+        xq = torch.empty((M, H), dtype=u8, device="cuda")
+        xqs = torch.empty((M, H // 32), dtype=u8, device="cuda")
+        aq = torch.empty((M, S_OIN), dtype=u8, device="cuda")
+        aqs = torch.empty((M, S_OIN // 32), dtype=u8, device="cuda")
+        tab = {n: torch.zeros(sz, dtype=i32, device="cuda") for n, sz in
+               [("counts", 2 * E), ("cta_batch", ctas), ("cta_limit", ctas), ("nne", 1), ("total_padded", 1),
+                ("route_map", rows), ("exp2perm", M * k)]}
+        c1 = torch.empty((rows, I), dtype=u8, device="cuda")
+        sf1 = torch.empty((rows // 128) * 512 * (-(-(I // 32) // 4)), dtype=u8, device="cuda")
+        c2 = torch.empty((rows, H), dtype=bf16, device="cuda")
+
+        def step():
+            x = x0
+            for l, L in enumerate(layers):
+                if M <= 16:  # decode: W4A16 GEMV straight from bf16
+                    ops.mxfp4_gemv_bf16(x, *L["qkv"], qkv, M, N=S_QKV, K=H)
+                    ops.mxfp4_gemv_bf16(attn, *L["o"], o[l], M, N=H, K=S_OIN)
+                else:
+                    ops.moe_quant(x, xq, xqs, M, K=H)
+                    ops.mxfp4_gemm_bf16(*L["qkv"], xq, xqs, qkv, M=M, m=S_QKV, k=H)
+                    ops.moe_quant(attn, aq, aqs, M, K=S_OIN)
+                    ops.mxfp4_gemm_bf16(*L["o"], aq, aqs, o[l], M=M, m=H, k=S_OIN)
+                ops.moe_quant(o[l], xq, xqs, M, K=H)
+                ops.moe_routing(ids[l], tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"],
+                                tab["total_padded"], tab["route_map"], tab["exp2perm"], tokens=M, topk=k,
+                                local_start=0, local_experts=E)
+                ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(*L["w13"], xq, xqs, c1, sf1, tab["route_map"], alpha, beta,
+                                                    tab["nne"], tab["total_padded"], tab["cta_batch"],
+                                                    tab["cta_limit"], m=2 * I, k=H, ctas=ctas)
+                ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(*L["w2"], c1, sf1, c2, tab["nne"], tab["total_padded"],
+                                                  tab["cta_batch"], tab["cta_limit"], m=H, k=I, ctas=ctas)
+                x = o[l]
+
+        n = max(3, min(steps, 50))
+        log(f"config 5: M={M}: capturing {n} steps through kern_graph_*")
+        for _ in range(max(1, min(warmup, 3))):
+            step()
+        torch.cuda.synchronize()
+        with ops.Graph() as g:
+            for _ in range(n):
+                step()
+        g.launch()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        g.launch()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / n
+        g.close()
+        R = M * k
+        hit = [len(set(a.reshape(-1).tolist())) for a in ids_np]
+        nbytes = sum(w_dense + h * per_expert for h in hit) + S_LAYERS * (
+            2 * M * (H + S_OIN + S_QKV + H) + R * H * 33 // 32 + R * I * 33 // 32 * 2 + R * H * 2)
+        flop = S_LAYERS * (2 * M * S_QKV * H + 2 * M * H * S_OIN + 2 * R * 2 * I * H + 2 * R * H * I)
+        res[f"M={M}"] = {"ms_per_step": round(ms, 5), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2), "algorithmic_bytes": nbytes,
+                         "algorithmic_flop": flop, "experts_hit_per_layer": hit, "cta_slots": ctas,
+                         "dense_path": "gemv" if M <= 16 else "quant + gemm"}
+        del tab, c1, sf1, c2, qkv, o, xq, xqs, aq, aqs
+        torch.cuda.synchronize()
+    return res
+
+
 def cpu_baseline_gemm(torch, wl, tensors):
     """The C oracle on the first rows of the same GEMM (bounded sample), fp32 accumulation."""
     import numpy as np
@@ -310,6 +426,10 @@ def main():
         torch.cuda.synchronize()
         if args.only in (None, "moe"):
             mo = bench_moe(torch, ops, wl, stream, args.steps, args.warmup)
+        torch.cuda.synchronize()
+        st = None
+        if args.only in (None, "stack"):
+            st = bench_stack(torch, ops, wl, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
 
     cpu = None
@@ -369,8 +489,13 @@ def main():
                           "algorithmic_bytes": g["quant_bytes"]},
             "decode": dec,
             "moe": moe,
+            "stack": None if st is None else {"metric": "config 5 layer stack (4 layers, hipGraph)", **st},
             "cpu_baseline": cpu,
         }
+    elif st is not None and dec is None and moe is None:
+        out = {"metric": "config 5 layer stack (4 layers, hipGraph)", **st}
+        out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+                    "scaling": "weak", "vs_baseline": None, "data": "synthetic"})
     else:
         out = dict(dec if dec is not None else moe)
         out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

@@ -327,3 +327,45 @@ def op_plan(op: dict | str, launch: int, params, vars: dict | None = None) -> di
                              ctypes.byref(size), ctypes.byref(skip)))
     return {"grid": tuple(grid), "block": tuple(block), "shared": shared.value,
             "args": bytes(buf[:size.value]) if not skip.value else b"", "skip": bool(skip.value)}
+
+
+# ----------------------------------------------------------------------------------- graphs
+
+class Graph:
+    """hipGraph of everything enqueued on torch's current stream inside the `with` block, captured
+    through kern_graph_begin / kern_graph_end (exec.rs:489-548) and replayed by launch()
+    (exec.rs:644-654). The stream must not be the null stream, and nothing inside the block may
+    allocate device memory (allocate first, as the reference runtime owns its buffers at var max)."""
+
+    def __init__(self):
+        self._g = None
+        self._stream = None
+
+    def __enter__(self):
+        self._stream = _stream()
+        check(lib().kern_graph_begin(self._stream))
+        return self
+
+    def __exit__(self, et, ev, tb):
+        g = ctypes.c_void_p()
+        rc = lib().kern_graph_end(self._stream, ctypes.byref(g))
+        if et is None:
+            check(rc)
+            self._g = g
+        return False
+
+    def launch(self):
+        if not self._g:
+            raise KernError(4, "graph was not captured")
+        check(lib().kern_graph_launch(self._g, _stream()))
+
+    def close(self):
+        if self._g:
+            lib().kern_graph_destroy(self._g)
+            self._g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
