@@ -18,15 +18,17 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
   copies (> 256 MB, the Infinity Cache) that every launch streams its weights from HBM; GB/s of
   algorithmic bytes against the 8 TB/s HBM peak.
 * `moe` = config 4: T=512 tokens, 256 experts, top-8, H=7168, I=2048. One step = moe_quant of the tokens,
-  moe_routing, FC1 (gate+up K=7168 -> 2I=4096, SiTU-GLU, MXFP8 out) and FC2 (K=2048 -> 7168, bf16 out),
+  moe_routing, FC1 (gate+up K=7168 -> 2I=4096, SiTU-GLU, MXFP8 out), FC2 (K=2048 -> 7168, bf16 out) and
+  moe_finalize_rms (weighted combine of each token's routed rows + RMS norm),
   with ~6 GB of repacked weights (every expert is hit), so each step streams its weights from HBM; GB/s of
   algorithmic bytes (weights of the experts hit + routed activations in and out) against the HBM peak,
   for the step and for FC1 and FC2 alone.
-* `stack` = config 5: four layers of (QKV [M,7168]x[9216,7168], O [M,8192]x[7168,8192], MoE as config 4)
+* `stack` = config 5: four layers of (QKV [M,7168]x[9216,7168], O [M,8192]x[7168,8192], MoE as config 4
+  through the finalize)
   at M = 1, 64, 2048, each program captured once through the library's own hipGraph C ABI
   (kern_graph_begin/end) and replayed. M <= 16 takes the decode GEMV for QKV and O, larger M quantizes
-  to MXFP8 and takes the GEMM; the O input stands in for attention (out of scope) and each layer's O
-  output feeds the next layer. Reported per M: step time, algorithmic HBM bytes (weights touched +
+  to MXFP8 and takes the GEMM; the O input stands in for attention (out of scope); the O output feeds
+  the layer's MoE and the finalized MoE output the next layer. Reported per M: step time, algorithmic HBM bytes (weights touched +
   activations) as GB/s and FLOPs as TFLOP/s.
 * `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on a bounded
   sample of the same GEMM (its first rows), in the headline unit.
@@ -216,6 +218,8 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
     w2, s2 = weights(41, MH, MI, False)
     alpha = torch.full((ME,), 4.0, dtype=torch.float32, device="cuda")
     beta = torch.full((ME,), 25.0, dtype=torch.float32, device="cuda")
+    tw = dev_from_np(wl.topk_weights(4, MT, MTOP), torch)
+    gamma = dev_from_np(wl.activations_bf16(5, 1, MH).reshape(-1), torch)
     ctas = ops.ctas_bound(MT, MTOP, ME)
     rows = ctas * 128
     i32 = torch.int32
@@ -227,6 +231,7 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
     c1 = torch.empty((rows, MI), dtype=u8, device="cuda")
     sf1 = torch.empty((rows // 128) * 512 * (-(-(MI // 32) // 4)), dtype=u8, device="cuda")  # R128c4
     c2 = torch.empty((rows, MH), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((MT, MH), dtype=torch.bfloat16, device="cuda")
     torch.cuda.synchronize()
 
     def route():
@@ -243,22 +248,29 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
         ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(w2, s2, c1, sf1, c2, tab["nne"], tab["total_padded"], tab["cta_batch"],
                                           tab["cta_limit"], m=MH, k=MI, ctas=ctas, sf_b_r128c4=True)
 
+    def finalize():
+        ops.moe_finalize_rms(c2, tab["exp2perm"], tw, gamma, y, MT, H=MH, topk=MTOP, eps=1e-6)
+
     def step(i):
         route()
         fc1()
         fc2()
+        finalize()
 
     log(f"config 4: timing {steps} steps after {warmup} warm-up")
     ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
     ms_fc1, _ = timed_loop(torch, stream, lambda i: fc1(), steps, warmup)
     ms_fc2, _ = timed_loop(torch, stream, lambda i: fc2(), steps, warmup)
+    ms_fin, _ = timed_loop(torch, stream, lambda i: finalize(), steps, warmup)
     hit = len(set(ids_np.reshape(-1).tolist()))
     R = MT * MTOP
     b_fc1 = hit * 2 * MI * MH * 17 // 32 + R * MH * 33 // 32 + R * MI * 33 // 32
     b_fc2 = hit * MH * MI * 17 // 32 + R * MI * 33 // 32 + R * MH * 2
-    b_step = b_fc1 + b_fc2 + MT * MH * 2 + MT * MH * 33 // 32 + MT * MTOP * 4
-    return {"ms_per_step": ms_step, "wall_ms_per_step": wall, "ms_fc1": ms_fc1, "ms_fc2": ms_fc2,
-            "bytes_fc1": b_fc1, "bytes_fc2": b_fc2, "bytes_step": b_step, "experts_hit": hit, "slots": ctas}
+    b_fin = R * MH * 2 + MT * MH * 2 + MH * 2 + R * 8
+    b_step = b_fc1 + b_fc2 + b_fin + MT * MH * 2 + MT * MH * 33 // 32 + MT * MTOP * 4
+    return {"ms_per_step": ms_step, "wall_ms_per_step": wall, "ms_fc1": ms_fc1, "ms_fc2": ms_fc2, "ms_fin": ms_fin,
+            "bytes_fc1": b_fc1, "bytes_fc2": b_fc2, "bytes_fin": b_fin, "bytes_step": b_step, "experts_hit": hit,
+            "slots": ctas}
 
 
 def bench_stack(torch, ops, wl, stream, steps, warmup):
@@ -298,6 +310,9 @@ def bench_stack(torch, ops, wl, stream, steps, warmup):
     for M in S_MS:
         ids_np = [wl.topk_ids(540 + l + 10 * M, M, E, k) for l in range(S_LAYERS)]
         ids = [torch.from_numpy(a).cuda() for a in ids_np]
+        tw = dev_from_np(wl.topk_weights(560 + M, M, k), torch)
+        gamma = dev_from_np(wl.activations_bf16(561, 1, H).reshape(-1), torch)
+        xs = [torch.empty((M, H), dtype=bf16, device="cuda") for _ in range(S_LAYERS)]
         x0 = dev_from_np(wl.activations_bf16(550 + M, M, H), torch)
         attn = dev_from_np(wl.activations_bf16(551 + M, M, S_OIN), torch)
         ctas = ops.ctas_bound(M, k, E)
@@ -335,7 +350,8 @@ def bench_stack(torch, ops, wl, stream, steps, warmup):
                                                     tab["cta_limit"], m=2 * I, k=H, ctas=ctas)
                 ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(*L["w2"], c1, sf1, c2, tab["nne"], tab["total_padded"],
                                                   tab["cta_batch"], tab["cta_limit"], m=H, k=I, ctas=ctas)
-                x = o[l]
+                ops.moe_finalize_rms(c2, tab["exp2perm"], tw, gamma, xs[l], M, H=H, topk=k, eps=1e-6)
+                x = xs[l]
 
         n = max(3, min(steps, 50))
         log(f"config 5: M={M}: capturing {n} steps through kern_graph_*")
@@ -357,14 +373,15 @@ def bench_stack(torch, ops, wl, stream, steps, warmup):
         R = M * k
         hit = [len(set(a.reshape(-1).tolist())) for a in ids_np]
         nbytes = sum(w_dense + h * per_expert for h in hit) + S_LAYERS * (
-            2 * M * (H + S_OIN + S_QKV + H) + R * H * 33 // 32 + R * I * 33 // 32 * 2 + R * H * 2)
+            2 * M * (H + S_OIN + S_QKV + H) + R * H * 33 // 32 + R * I * 33 // 32 * 2 + R * H * 2
+            + R * H * 2 + M * H * 2)
         flop = S_LAYERS * (2 * M * S_QKV * H + 2 * M * H * S_OIN + 2 * R * 2 * I * H + 2 * R * H * I)
         res[f"M={M}"] = {"ms_per_step": round(ms, 5), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                          "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                          "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2), "algorithmic_bytes": nbytes,
                          "algorithmic_flop": flop, "experts_hit_per_layer": hit, "cta_slots": ctas,
                          "dense_path": "gemv" if M <= 16 else "quant + gemm"}
-        del tab, c1, sf1, c2, qkv, o, xq, xqs, aq, aqs
+        del tab, c1, sf1, c2, qkv, o, xq, xqs, aq, aqs, xs
         torch.cuda.synchronize()
     return res
 
@@ -461,9 +478,10 @@ def main():
         moe = {"metric": "MoE grouped step GB/s (config 4)", "value": round(gbs, 1), "unit": "GB/s",
                "ms_per_step": round(mo["ms_per_step"], 5), "frac": round(gbs / PEAK_HBM_GBS, 4),
                "algorithmic_bytes": mo["bytes_step"],
-               "step": "moe_quant + moe_routing + moe_fc1 + moe_fc2",
+               "step": "moe_quant + moe_routing + moe_fc1 + moe_fc2 + moe_finalize_rms",
                "fc1": hbm(mo["bytes_fc1"], mo["ms_fc1"], "kern_mx_bmm_fc1"),
                "fc2": hbm(mo["bytes_fc2"], mo["ms_fc2"], "kern_mx_bmm_fc2"),
+               "finalize": hbm(mo["bytes_fin"], mo["ms_fin"], "kern_mx_moe_finalize_rms"),
                "config": {"T": MT, "E": ME, "topk": MTOP, "H": MH, "I": MI, "experts_hit": mo["experts_hit"],
                           "cta_slots": mo["slots"]}}
 

@@ -208,6 +208,24 @@ int kern_mxfp4_gemm_bf16(const void* a, const void* sf_a, const void* b, const v
 int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_sf, void* y, int32_t M, int32_t N, int32_t K,
                          void* stream);
 
+/* silu_mul (tools/kernels-src/silu_mul.cu:1-36, kernel ABI (out, in, d), grid [tokens, ceil(d/2048)]):
+ * out bf16 [tokens][d] = bf16(bf16(g / (1 + exp(-g))) * u), g = in[t][i], u = in[t][d + i], in bf16
+ * [tokens][2d]. d % 8 == 0. */
+int kern_silu_mul(void* out, const void* in, int32_t tokens, int32_t d, void* stream);
+
+/* moe_finalize_rms (fixtures/k3/head.json op moe_finalize_rms, call l1.finalize: fc2_out, exp2perm,
+ * topk_weight, gamma, out, tokens; the launch adds H, topk and eps): y[t] = sum_j topk_weight[t][j] *
+ * fc2_out[exp2perm[t*topk + j]] in j order with f32 FMAs (exp2perm < 0: a non-local expert, skipped),
+ * the combine of tools/trtllm-bmm/probe.py:100-110; out[t] = bf16(y / sqrt(mean(y^2) + eps) * gamma).
+ * 0 < H <= 8192, H % 8 == 0. The reference kernel's source is not in its tree: the norm's eps and weight
+ * convention are this build's. */
+int kern_moe_finalize_rms(const void* fc2_out, const int32_t* exp2perm, const float* topk_weight, const void* gamma,
+                          void* out, int32_t tokens, int32_t H, int32_t topk, float eps, void* stream);
+
+/* The same combine without the norm: out[t] = bf16(y) (flashinfer's do_finalize, probe.py:85-110). */
+int kern_moe_finalize(const void* fc2_out, const int32_t* exp2perm, const float* topk_weight, void* out,
+                      int32_t tokens, int32_t H, int32_t topk, void* stream);
+
 /* Seeded synthetic bytes: out[i] = lo + splitmix64_i(seed) % span (crates/kern-test/src/workload.rs:11-26). */
 int kern_fill_random_u8(void* out, int64_t n, uint64_t seed, int32_t lo, int32_t span, void* stream);
 

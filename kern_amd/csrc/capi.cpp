@@ -474,6 +474,45 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
   return launch("kern_mx_gemv_bf16", (uint32_t)(N / 16), 1, 1, 256, stream, a, lds);
 }
 
+extern "C" int kern_silu_mul(void* out, const void* in, int32_t tokens, int32_t d, void* stream) {
+  REQUIRE(tokens >= 0 && d > 0 && d % 8 == 0, "silu_mul: need d > 0, d %% 8 == 0, tokens >= 0 (d=%d tokens=%d)", d,
+          tokens);
+  if (tokens == 0) return KERN_OK;
+  REQUIRE(out && in, "silu_mul: null buffer");
+  REQUIRE(tokens <= 0x7fffffff && (d + 2047) / 2048 <= 65535, "silu_mul: grid too large (d=%d)", d);
+  Args a;
+  a.put(out), a.put(in), a.put(d);
+  kern_function f = nullptr;
+  if (int rc = function("kern_silu_mul_bf16", &f)) return rc;
+  if (int rc = kern_function_check_params(f, a.sizes.data(), (int)a.sizes.size())) return rc;
+  const uint32_t grid[3] = {(uint32_t)tokens, (uint32_t)((d + 2047) / 2048), 1}, blk[3] = {256, 1, 1};
+  return kern_launch(f, grid, blk, 0, stream, a.buf, (a.n + 7) & ~size_t(7));
+}
+
+extern "C" int kern_moe_finalize_rms(const void* fc2_out, const int32_t* exp2perm, const float* topk_weight,
+                                     const void* gamma, void* out, int32_t tokens, int32_t H, int32_t topk, float eps,
+                                     void* stream) {
+  REQUIRE(tokens >= 0 && H > 0 && H % 8 == 0 && H <= 8192 && topk > 0 && eps >= 0.f,
+          "moe_finalize_rms: need 0 < H <= 8192, H %% 8 == 0, topk > 0, eps >= 0 (H=%d topk=%d)", H, topk);
+  if (tokens == 0) return KERN_OK;
+  REQUIRE(fc2_out && exp2perm && topk_weight && gamma && out, "moe_finalize_rms: null buffer");
+  Args a;
+  a.put(fc2_out), a.put(exp2perm), a.put(topk_weight), a.put(gamma), a.put(out), a.put(tokens), a.put(H);
+  a.put(topk), a.put(eps);
+  return launch("kern_mx_moe_finalize_rms", (uint32_t)tokens, 1, 1, 256, stream, a);
+}
+
+extern "C" int kern_moe_finalize(const void* fc2_out, const int32_t* exp2perm, const float* topk_weight, void* out,
+                                 int32_t tokens, int32_t H, int32_t topk, void* stream) {
+  REQUIRE(tokens >= 0 && H > 0 && H % 8 == 0 && topk > 0, "moe_finalize: need H > 0, H %% 8 == 0, topk > 0 (H=%d topk=%d)",
+          H, topk);
+  if (tokens == 0) return KERN_OK;
+  REQUIRE(fc2_out && exp2perm && topk_weight && out, "moe_finalize: null buffer");
+  Args a;
+  a.put(fc2_out), a.put(exp2perm), a.put(topk_weight), a.put(out), a.put(tokens), a.put(H), a.put(topk);
+  return launch("kern_mx_moe_finalize", (uint32_t)tokens, 1, 1, 256, stream, a);
+}
+
 extern "C" int kern_fill_random_u8(void* out, int64_t n, uint64_t seed, int32_t lo, int32_t span, void* stream) {
   REQUIRE(n >= 0 && span >= 1 && span <= 256, "fill_random_u8: need n >= 0 and 1 <= span <= 256");
   if (n == 0) return KERN_OK;

@@ -793,6 +793,121 @@ extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
   }
 }
 
+// ====================================================================================== MoE glue
+// silu_mul (tools/kernels-src/silu_mul.cu:1-5): out[t][i] = bf16(bf16(g / (1 + exp(-g))) * u), g = in[t][i],
+// u = in[t][d + i]; in [tokens][2d], out [tokens][d] (bf16). Same ABI as the reference kernel: (out, in, d),
+// grid [tokens, ceil(d / 2048)], block 256, eight consecutive elements per thread (one 16-byte load per
+// operand); d % 8 == 0. SiLU in f32 with an IEEE divide, rounded to bf16; the product of two bf16 values
+// is exact in f32 and rounded once.
+extern "C" __global__ __launch_bounds__(256) void kern_silu_mul_bf16(uint16_t* __restrict__ out,
+                                                                     const uint16_t* __restrict__ in, int d) {
+  const int64_t t = blockIdx.x;
+  const int i = (blockIdx.y * 256 + threadIdx.x) * 8;
+  if (i >= d) return;
+  const v4u gv = *reinterpret_cast<const v4u*>(in + t * 2 * d + i);
+  const v4u uv = *reinterpret_cast<const v4u*>(in + t * 2 * d + d + i);
+  v4u ov;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float g = bf16_bits_to_f32((gv[j] >> (16 * h)) & 0xffffu);
+      const float u = bf16_bits_to_f32((uv[j] >> (16 * h)) & 0xffffu);
+      const float sl = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.0f + expf(-g))));
+      o |= f32_to_bf16_bits(sl * u) << (16 * h);
+    }
+    ov[j] = o;
+  }
+  *reinterpret_cast<v4u*>(out + t * d + i) = ov;
+}
+
+// MoE finalize: y[t] = sum_j w[t][j] * fc2_out[exp2perm[t*topk + j]] over the token's routed rows in j order
+// (f32 fused multiply-adds; rows of non-local experts, exp2perm < 0, add nothing), the combine of
+// tools/trtllm-bmm/probe.py:100-110 (index_add of weighted FC2 rows). moe_finalize_rms (head.json: module
+// k3_prefill_glue, entry kern_k3g_finalize_rms) then writes out[t] = bf16(y * (1 / sqrt(mean(y^2) + eps)) *
+// gamma), the plain finalize out[t] = bf16(y). One workgroup of 256 threads per token, eight consecutive
+// columns per thread and chunk; H % 8 == 0 and, with the norm, H <= 8192 (the row stays in registers
+// between the two passes).
+// the combined row y of one 8-column chunk of token t
+KERN_DEV void moe_combine_chunk(const uint16_t* __restrict__ fc2_out, const int* __restrict__ exp2perm,
+                                const float* __restrict__ topk_w, int t, int H, int topk, int chunk, float acc[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int j = 0; j < topk; ++j) {
+    const int row = exp2perm[(int64_t)t * topk + j];
+    const float w = topk_w[(int64_t)t * topk + j];
+    if (row < 0) continue;
+    const v4u xv = *reinterpret_cast<const v4u*>(fc2_out + (int64_t)row * H + chunk * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      acc[e] = __builtin_fmaf(w, bf16_bits_to_f32((xv[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+  }
+}
+
+KERN_DEV v4u bf16x8(const float v[8]) {
+  v4u o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16_bits(v[2 * e]) | (f32_to_bf16_bits(v[2 * e + 1]) << 16);
+  return o;
+}
+
+// op moe_finalize_rms (head.json, call l1.finalize): in bf16 fc2_out [padded][H], in i32 exp2perm [T*topk],
+// in f32 topk_weight [T][topk], in bf16 gamma [H], out bf16 out [T][H], i32 T; launch adds i32 H, i32 topk,
+// f32 eps. Grid [T], block 256.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize_rms(
+    const uint16_t* __restrict__ fc2_out, const int* __restrict__ exp2perm, const float* __restrict__ topk_w,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int T, int H, int topk, float eps) {
+  __shared__ float red[4];
+  (void)T;
+  const int t = blockIdx.x, tid = threadIdx.x, chunks = H >> 3;
+  constexpr int Q = 4;  // chunks per thread kept in registers between the passes (H <= 8192)
+  float y[Q][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int c = tid + 256 * q;
+    if (c < chunks) {
+      moe_combine_chunk(fc2_out, exp2perm, topk_w, t, H, topk, c, y[q]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[q][e], y[q][e], ss);
+    }
+  }
+  // sum of squares over the row: wave reduction, then the four waves in LDS
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float r = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int c = tid + 256 * q;
+    if (c < chunks) {
+      const v4u gm = *reinterpret_cast<const v4u*>(gamma + c * 8);
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = y[q][e] * r * bf16_bits_to_f32((gm[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      *reinterpret_cast<v4u*>(out + (int64_t)t * H + c * 8) = bf16x8(v);
+    }
+  }
+}
+
+// MoE finalize without the norm (the combine flashinfer's do_finalize returns, probe.py:85-110):
+// fc2_out, exp2perm, topk_weight, out bf16 [T][H], i32 T; launch adds i32 H, i32 topk. Grid [T], block 256.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize(const uint16_t* __restrict__ fc2_out,
+                                                                       const int* __restrict__ exp2perm,
+                                                                       const float* __restrict__ topk_w,
+                                                                       uint16_t* __restrict__ out, int T, int H,
+                                                                       int topk) {
+  (void)T;
+  const int t = blockIdx.x;
+  for (int c = threadIdx.x; c < (H >> 3); c += 256) {
+    float v[8];
+    moe_combine_chunk(fc2_out, exp2perm, topk_w, t, H, topk, c, v);
+    *reinterpret_cast<v4u*>(out + (int64_t)t * H + c * 8) = bf16x8(v);
+  }
+}
+
 // ====================================================================================== workload fills
 // Synthetic seeded inputs (splitmix64 stream, crates/kern-test/src/workload.rs:11-26):
 // out[i] = lo + draw_i % span.

@@ -129,8 +129,25 @@ def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
     }
 
 
+def moe_finalize_rms(H: int, topk: int, eps: float = 1e-6) -> dict:
+    """moe_finalize_rms(in bf16 fc2_out, in i32 exp2perm, in f32 topk_weight, in bf16 gamma, out bf16 out,
+    i32 T); launch adds i32 H, i32 topk and f32 eps. One workgroup per token (grid.x = tokens)."""
+    assert H % 8 == 0 and H <= 8192
+    p = ["in buffer<bf16>", "in buffer<i32>", "in buffer<f32>", "in buffer<bf16>", "out buffer<bf16>", "i32"]
+    return {
+        "params": p,
+        "impl": {"launches": [{
+            "module": MODULE, "entry": "kern_mx_moe_finalize_rms",
+            "params": p + ["i32", "i32", "f32"],
+            "block": [256, 1, 1],
+            "grid": [{"mul": ["tokens", 1]}, 1, 1],
+            "args": [{"param": i} for i in range(6)] + [{"i32": H}, {"i32": topk}, {"f32": eps}],
+        }]},
+    }
+
+
 def moe_ops(H: int, I: int, E: int, topk: int, local_start: int = 0) -> dict:
-    """The six ops of one MoE layer (hidden H, intermediate I, E local experts, top-k) as `ops` entries."""
+    """The ops of one MoE layer (hidden H, intermediate I, E local experts, top-k) as `ops` entries."""
     return {
         "moe_quant": moe_quant(H),
         "k3_moe_w_shuffle": k3_moe_w_shuffle(E, max(2 * I * H // 2, H * I // 2)),
@@ -138,4 +155,5 @@ def moe_ops(H: int, I: int, E: int, topk: int, local_start: int = 0) -> dict:
         "moe_routing": moe_routing(topk, local_start, E),
         "moe_fc1": moe_fc1(2 * I, H, E, topk),
         "moe_fc2": moe_fc2(H, I, E, topk),
+        "moe_finalize_rms": moe_finalize_rms(H, topk),
     }

@@ -48,6 +48,9 @@ _SIGS = {
     "kern_mxfp4_gemm_bf16": [P] * 5 + [I32, I32, I32, P, P],
     "kern_mxfp4_gemv_bf16": [P] * 4 + [I32, I32, I32, P],
     "kern_fill_random_u8": [P, I64, ctypes.c_uint64, I32, I32, P],
+    "kern_silu_mul": [P, P, I32, I32, P],
+    "kern_moe_finalize_rms": [P] * 5 + [I32, I32, I32, ctypes.c_float, P],
+    "kern_moe_finalize": [P] * 4 + [I32, I32, I32, P],
     "kern_init": [ctypes.c_char_p],
     "kern_sha256_hex": [P, ctypes.c_size_t, ctypes.c_char_p],
     "kern_code_object_param_sizes": [P, ctypes.c_size_t, ctypes.c_char_p, P, ctypes.c_int, P],
@@ -211,6 +214,29 @@ def mxfp4_gemv_bf16(x, w, w_sf, y, M, *, N, K):
     check(lib().kern_mxfp4_gemv_bf16(
         _ptr(x, "x", bf16, M * K), _ptr(w, "w", u8, N * K // 2), _ptr(w_sf, "w_sf", u8, N * K // 32),
         _ptr(y, "y", bf16, M * N), M, N, K, _stream()))
+
+
+def silu_mul(out, x, tokens, d):
+    """silu_mul (tools/kernels-src/silu_mul.cu): out bf16 [tokens, d] = bf16(bf16(silu(g)) * u) over
+    x bf16 [tokens, 2d] = [g | u]."""
+    check(lib().kern_silu_mul(_ptr(out, "out", bf16, tokens * d), _ptr(x, "x", bf16, tokens * 2 * d), tokens, d,
+                              _stream()))
+
+
+def moe_finalize_rms(fc2_out, exp2perm, topk_weight, gamma, out, tokens, *, H, topk, eps=1e-6):
+    """moe_finalize_rms (fixtures/k3/head.json): out[t] = bf16(rms_norm(sum_j w[t,j] * fc2_out[exp2perm[t,j]]) * gamma)."""
+    check(lib().kern_moe_finalize_rms(
+        _ptr(fc2_out, "fc2_out", bf16), _ptr(exp2perm, "exp2perm", i32, tokens * topk),
+        _ptr(topk_weight, "topk_weight", f32, tokens * topk), _ptr(gamma, "gamma", bf16, H),
+        _ptr(out, "out", bf16, tokens * H), tokens, H, topk, float(eps), _stream()))
+
+
+def moe_finalize(fc2_out, exp2perm, topk_weight, out, tokens, *, H, topk):
+    """MoE finalize without the norm: out[t] = bf16(sum_j w[t,j] * fc2_out[exp2perm[t,j]])."""
+    check(lib().kern_moe_finalize(
+        _ptr(fc2_out, "fc2_out", bf16), _ptr(exp2perm, "exp2perm", i32, tokens * topk),
+        _ptr(topk_weight, "topk_weight", f32, tokens * topk), _ptr(out, "out", bf16, tokens * H), tokens, H, topk,
+        _stream()))
 
 
 def fill_random_u8(out, seed, lo=0, span=256):

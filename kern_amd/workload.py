@@ -86,3 +86,10 @@ def topk_ids(seed: int, T: int, E: int, k: int) -> np.ndarray:
             p[j], p[r] = p[r], p[j]
         out[t] = p[:k]
     return out
+
+
+def topk_weights(seed: int, T: int, k: int) -> np.ndarray:
+    """Per token, k positive routing weights summing to one (uniform draws in [0.1, 1.1), normalised), f32."""
+    d = draws(tensor_seed(seed, 6), T * k).reshape(T, k)
+    w = (d >> np.uint64(11)).astype(np.float64) * 2.0**-53 + 0.1
+    return (w / w.sum(1, keepdims=True)).astype(np.float32)

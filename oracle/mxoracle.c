@@ -368,6 +368,34 @@ void mxo_silu_mul_bf16(const uint16_t* in, int64_t T, int64_t d, uint16_t* out) 
     }
 }
 
+/* MoE finalize (tools/trtllm-bmm/probe.py:100-110: index_add of the weighted FC2 rows of each token):
+ * y[t][h] = sum_j w[t][j] * fc2[e2p[t*topk + j]][h], j ascending, f32 fused multiply-adds, rows with
+ * e2p < 0 (non-local experts) skipped. gamma == NULL: out = bf16(y). Otherwise the norm of op
+ * moe_finalize_rms: out = bf16(y * (1 / sqrt(ss / H + eps)) * gamma), ss = sum of y^2 over the row in
+ * column order (f32 FMAs). */
+void mxo_moe_finalize(const uint16_t* fc2, const int32_t* e2p, const float* w, const uint16_t* gamma, int64_t T,
+                      int64_t H, int topk, float eps, uint16_t* out) {
+  float* y = (float*)malloc(sizeof(float) * (size_t)H);
+  for (int64_t t = 0; t < T; ++t) {
+    for (int64_t h = 0; h < H; ++h) y[h] = 0.f;
+    for (int j = 0; j < topk; ++j) {
+      int32_t row = e2p[t * topk + j];
+      float wj = w[t * topk + j];
+      if (row < 0) continue;
+      for (int64_t h = 0; h < H; ++h) y[h] = fmaf(wj, mxo_bf16_to_f32(fc2[(int64_t)row * H + h]), y[h]);
+    }
+    if (!gamma) {
+      for (int64_t h = 0; h < H; ++h) out[t * H + h] = mxo_f32_to_bf16(y[h]);
+      continue;
+    }
+    float ss = 0.f;
+    for (int64_t h = 0; h < H; ++h) ss = fmaf(y[h], y[h], ss);
+    float r = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int64_t h = 0; h < H; ++h) out[t * H + h] = mxo_f32_to_bf16(y[h] * r * mxo_bf16_to_f32(gamma[h]));
+  }
+  free(y);
+}
+
 /* --------------------------------------------------------------- routing */
 
 int64_t mxo_max_ctas(int64_t tokens, int topk, int experts, int tile) {

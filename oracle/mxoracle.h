@@ -103,6 +103,12 @@ float mxo_situ(float g, float u, float alpha, float beta);
 /* out[t][i] = bf16(bf16(g/(1+exp(-g))) * u), g = in[t][i], u = in[t][d+i]  (tools/kernels-src/silu_mul.cu:1-5) */
 void mxo_silu_mul_bf16(const uint16_t* in, int64_t T, int64_t d, uint16_t* out);
 
+/* MoE finalize: y[t] = sum_j w[t][j] * fc2[e2p[t*topk+j]] (j ascending, f32 FMAs, e2p < 0 skipped)
+ * (tools/trtllm-bmm/probe.py:100-110); gamma == NULL: out = bf16(y), else out = bf16(y / sqrt(mean(y^2) +
+ * eps) * gamma) (op moe_finalize_rms; parity unpinned: the reference kernel's source is absent). */
+void mxo_moe_finalize(const uint16_t* fc2, const int32_t* e2p, const float* w, const uint16_t* gamma, int64_t T,
+                      int64_t H, int topk, float eps, uint16_t* out);
+
 /* ---- routing tables (tools/kernels/abi/trtllm_bmm.py:19-27, :50-60; op moe_routing head.json:25117) ----
  * topk_idx: i32 [T][topk] global expert ids. Local experts are [local_start, local_start+E_local).
  * Expanded index i = t*topk + j. For local expert e: counts[e] = rows routed to it; it owns

@@ -81,6 +81,7 @@ def _declare(L):
     L.mxo_gemm_f32.argtypes = [P, P, I64, I64, I64, P, I32]
     L.mxo_gemv_w4a16.argtypes = [P, P, P, I64, I64, I64, P, P, I32]
     L.mxo_silu_mul_bf16.argtypes = [P, I64, I64, P]
+    L.mxo_moe_finalize.argtypes = [P, P, P, P, I64, I64, I32, ctypes.c_float, P]
     L.mxo_routing.argtypes = [P, I64, I32, I32, I32, I32, P, P, P, P, P, P, P]
     L.mxo_max_ctas.restype = I64
     L.mxo_max_ctas.argtypes = [I64, I32, I32, I32]
@@ -266,6 +267,18 @@ def silu_mul_bf16(x_bf16, d):
     T = x.shape[0]
     out = np.empty((T, d), np.uint16)
     lib().mxo_silu_mul_bf16(_p(x), T, d, _p(out))
+    return out
+
+
+def moe_finalize(fc2_bf16, exp2perm, topk_weight, gamma_bf16, T, H, topk, eps=0.0):
+    """MoE finalize (mxo_moe_finalize): fc2 bf16 bits [rows][H], exp2perm i32 [T*topk], topk_weight f32
+    [T][topk], gamma bf16 bits [H] or None -> bf16 bits [T][H]."""
+    fc2 = _c(fc2_bf16, np.uint16)
+    e2p = _c(exp2perm, np.int32)
+    w = _c(topk_weight, np.float32)
+    g = None if gamma_bf16 is None else _c(gamma_bf16, np.uint16)
+    out = np.empty((T, H), np.uint16)
+    lib().mxo_moe_finalize(_p(fc2), _p(e2p), _p(w), None if g is None else _p(g), T, H, topk, float(eps), _p(out))
     return out
 
 

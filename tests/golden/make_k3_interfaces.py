@@ -8,7 +8,7 @@ import json
 import os
 import sys
 
-OPS = ["moe_quant", "k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_routing", "moe_fc1", "moe_fc2"]
+OPS = ["moe_quant", "k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_routing", "moe_fc1", "moe_fc2", "moe_finalize_rms"]
 
 
 def main(ref):
@@ -19,7 +19,7 @@ def main(ref):
     for name in OPS:
         op = m["ops"][name]
         rec = {"params": op["params"]}
-        if name in ("k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_fc1", "moe_fc2"):
+        if name in ("k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_fc1", "moe_fc2", "moe_finalize_rms"):
             rec["grid"] = op["impl"]["launches"][0]["grid"]
         out["ops"][name] = rec
     dst = os.path.join(os.path.dirname(os.path.abspath(__file__)), "k3_op_interfaces.json")

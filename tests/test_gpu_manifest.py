@@ -40,6 +40,8 @@ def test_moe_layer_through_manifest_ops(ops):
     ids = _dev(wl.topk_ids(72, T, E, k))
     w13, s13 = (_dev(a) for a in wl.mxfp4_weights(73, E, 2 * I, H, 119, 124))
     w2, s2 = (_dev(a) for a in wl.mxfp4_weights(74, E, H, I, 119, 124))
+    tw = torch.rand((T, k), device="cuda") + 0.1
+    gamma = _dev(wl.f32_to_bf16_bits(np.linspace(0.5, 1.5, H).astype(np.float32)))
     alpha = torch.full((E,), 4.0, device="cuda")
     beta = torch.full((E,), 25.0, device="cuda")
     ctas = ops.ctas_bound(T, k, E)
@@ -54,6 +56,7 @@ def test_moe_layer_through_manifest_ops(ops):
         c1 = torch.zeros((rows, I), dtype=u8, device="cuda")
         sf1 = torch.zeros(_r128c4_bytes(rows, I // 32), dtype=u8, device="cuda")
         c2 = torch.zeros((rows, H), dtype=torch.bfloat16, device="cuda")
+        fin = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
         counts, cb, cl, nne, tp, rmap, e2p = tabs
         if manifest:
             man["moe_quant"](x, out["q"], out["qs"], T, vars=v)
@@ -65,6 +68,7 @@ def test_moe_layer_through_manifest_ops(ops):
             man["moe_fc1"](out["w13"], out["s13"], out["q"], out["qs"], c1, sf1, rmap, alpha, beta, nne, tp, cb, cl,
                            vars=v)
             man["moe_fc2"](out["w2"], out["s2"], c1, sf1, c2, nne, tp, cb, cl, vars=v)
+            man["moe_finalize_rms"](c2, e2p, tw, gamma, fin, T, vars=v)
         else:
             ops.moe_quant(x, out["q"], out["qs"], T, K=H)
             ops.k3_moe_w_shuffle(w13, out["w13"], 2 * I, H // 2, True, experts=E)
@@ -75,9 +79,10 @@ def test_moe_layer_through_manifest_ops(ops):
             ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(out["w13"], out["s13"], out["q"], out["qs"], c1, sf1, rmap, alpha, beta,
                                                 nne, tp, cb, cl, m=2 * I, k=H, ctas=ctas)
             ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(out["w2"], out["s2"], c1, sf1, c2, nne, tp, cb, cl, m=H, k=I, ctas=ctas)
+            ops.moe_finalize_rms(c2, e2p, tw, gamma, fin, T, H=H, topk=k, eps=1e-6)
         torch.cuda.synchronize()
         out.update({f"tab{i}": t for i, t in enumerate(tabs)})
-        out.update({"c1": c1, "sf1": sf1, "c2": c2})
+        out.update({"c1": c1, "sf1": sf1, "c2": c2, "fin": fin})
         return out
 
     a, b = run(False), run(True)

@@ -270,3 +270,74 @@ def test_fc2_bf16(ops, oracle, T, E, k, m, K):
         _, acc = oracle.fc2(wpn.reshape(-1)[e * per_e:(e + 1) * per_e], sfpn.reshape(-1)[e * per_e // 16:(e + 1) * per_e // 16],
                             q_lin[r0:r0 + 128], qs_lin[r0:r0 + 128], False, sub, m, K)
         assert_gemm_close(got[r0:lim], acc[:lim - r0], f"fc2 slot {s}")
+
+
+# --------------------------------------------------------------------------------------- MoE glue
+
+def _ulp(a, b):
+    ai, bi = a.astype(np.int32), b.astype(np.int32)
+    oa = np.where(ai & 0x8000, -(ai & 0x7FFF), ai)
+    ob = np.where(bi & 0x8000, -(bi & 0x7FFF), bi)
+    return np.abs(oa - ob)
+
+
+@pytest.fixture(scope="module")
+def oracle():
+    from oracle import mxoracle
+    mxoracle.lib()
+    return mxoracle
+
+
+@pytest.mark.parametrize("T,d", [(7, 2056), (64, 2048), (3, 8), (512, 7168)])
+def test_silu_mul(ops, oracle, T, d):
+    x = wl.activations_bf16(300 + d, T, 2 * d)
+    if T == 7:  # special values in the gate half
+        f = wl.bf16_bits_to_f32(x).copy()
+        f[0, :6] = [np.inf, -np.inf, np.nan, 0.0, -100.0, 100.0]
+        f[1, :4] = [88.0, -88.0, 1e-30, -1e-30]
+        x = wl.f32_to_bf16_bits(f)
+    out = torch.zeros((T, d), dtype=torch.bfloat16, device="cuda")
+    ops.silu_mul(out, to_dev(x), T, d)
+    _sync()
+    got = to_np(out).view(np.uint16)
+    ref = oracle.silu_mul_bf16(x, d)
+    nan_g, nan_r = np.isnan(wl.bf16_bits_to_f32(got)), np.isnan(wl.bf16_bits_to_f32(ref))
+    np.testing.assert_array_equal(nan_g, nan_r)
+    fin = ~nan_r
+    # exp is the platform's (ocml on the GPU, libm here): results agree to one bf16 ulp, almost all exactly
+    d_ulp = _ulp(got[fin], ref[fin])
+    assert d_ulp.max() <= 1
+    assert (d_ulp == 0).mean() > 0.999
+
+
+def _finalize_case(T, H, k, rows, seed):
+    rng = np.random.default_rng(seed)
+    fc2 = wl.f32_to_bf16_bits(rng.standard_normal((rows, H)).astype(np.float32))
+    e2p = rng.permutation(rows)[: T * k].astype(np.int32)
+    e2p[5 % e2p.size] = -1  # a non-local expert
+    w = rng.random((T, k)).astype(np.float32) + 0.05
+    w /= w.sum(1, keepdims=True)
+    return fc2, e2p, w
+
+
+@pytest.mark.parametrize("T,H,k", [(512, 7168, 8), (9, 3584, 16), (3, 64, 2)])
+def test_moe_finalize_bitexact(ops, oracle, T, H, k):
+    rows = ((T * k + 127) // 128 + 4) * 128
+    fc2, e2p, w = _finalize_case(T, H, k, rows, 40 + H)
+    out = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
+    ops.moe_finalize(to_dev(fc2), to_dev(e2p), to_dev(w), out, T, H=H, topk=k)
+    _sync()
+    np.testing.assert_array_equal(to_np(out).view(np.uint16), oracle.moe_finalize(fc2, e2p, w, None, T, H, k))
+
+
+@pytest.mark.parametrize("T,H,k", [(512, 7168, 8), (9, 3584, 16), (3, 8192, 2)])
+def test_moe_finalize_rms(ops, oracle, T, H, k):
+    rows = ((T * k + 127) // 128 + 4) * 128
+    fc2, e2p, w = _finalize_case(T, H, k, rows, 50 + H)
+    gamma = wl.f32_to_bf16_bits((np.random.default_rng(H).random(H) + 0.5).astype(np.float32))
+    out = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
+    ops.moe_finalize_rms(to_dev(fc2), to_dev(e2p), to_dev(w), to_dev(gamma), out, T, H=H, topk=k, eps=1e-6)
+    _sync()
+    ref = oracle.moe_finalize(fc2, e2p, w, gamma, T, H, k, 1e-6)
+    # the combine is exact; the row's sum of squares is reduced in another order: one bf16 ulp at most
+    assert _ulp(to_np(out).view(np.uint16), ref).max() <= 1

@@ -60,6 +60,8 @@ def test_k3_grids_match_reference():
     # the CTA-slot axis of both GEMMs is the reference's expression, verbatim
     for name in ("moe_fc1", "moe_fc2"):
         assert o[name]["impl"]["launches"][0]["grid"][1] == g[name]["grid"][1], name
+    # one workgroup per token for the finalize, as the reference launches it
+    assert o["moe_finalize_rms"]["impl"]["launches"][0]["grid"] == g["moe_finalize_rms"]["grid"]
 
 
 @pytest.mark.parametrize("T", [1, 37, 512, 8192])
@@ -86,6 +88,10 @@ def test_plan_grids_and_kernargs(lib, shape, T):
     p = ops.op_plan(o["moe_fc2"], 0, bufs(9), v)
     assert p["grid"] == (H // 256, slots, 1)
     assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(9)] + [("i", H), ("i", I), ("i", 1), ("q", 0)])
+
+    p = ops.op_plan(o["moe_finalize_rms"], 0, bufs(5) + [T], v)
+    assert p["grid"] == (T, 1, 1) and p["block"] == (256, 1, 1)
+    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(5)] + [("i", T), ("i", H), ("i", k), ("f", 1e-6)])
 
     for name, rows, rb, gated in [("k3_moe_w_shuffle", 2 * I, H // 2, 1), ("k3_moe_sf_shuffle", H, I // 32, 0)]:
         p = ops.op_plan(o[name], 0, bufs(2) + [rows, rb, gated], v)
