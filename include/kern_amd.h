@@ -226,6 +226,24 @@ int kern_moe_finalize_rms(const void* fc2_out, const int32_t* exp2perm, const fl
 int kern_moe_finalize(const void* fc2_out, const int32_t* exp2perm, const float* topk_weight, void* out,
                       int32_t tokens, int32_t H, int32_t topk, void* stream);
 
+/* weight_prep family (tools/kernels-src/weight_prep.cu:1-70): the derived tables a manifest's `once`
+ * program builds after load; same entries and one-thread-per-element mapping as the reference's module,
+ * here launched with 256-thread workgroups over n elements.
+ *   weight_p1_bf16_f32: out[i] = f32(w[i]) + 1      cast_bf16_f32: out[i] = f32(w[i])
+ *   rope_table_bf16:    cos/sin[r*stride + j] = bf16(cos/sin(r / base^(2j/(2 half)))), r < rows, j < half
+ *   fill_{f32,i32,i64,u8,bf16}: p[i] = v (bf16: RNE of v; fill_bf16 is K3's k3_weight_prep entry)
+ *   iota_i32:           p[i*stride] = start + i*step */
+int kern_weight_p1_bf16_f32(const void* w, float* out, int32_t n, void* stream);
+int kern_cast_bf16_f32(const void* w, float* out, int32_t n, void* stream);
+int kern_rope_table_bf16(void* cos_t, void* sin_t, int32_t rows, int32_t half, int32_t stride, float base,
+                         void* stream);
+int kern_fill_f32(float* p, int32_t n, float v, void* stream);
+int kern_fill_i32(int32_t* p, int32_t n, int32_t v, void* stream);
+int kern_fill_i64(int64_t* p, int32_t n, int64_t v, void* stream);
+int kern_fill_u8(uint8_t* p, int32_t n, int32_t v, void* stream);
+int kern_fill_bf16(void* p, int32_t n, float v, void* stream);
+int kern_iota_i32(int32_t* p, int32_t n, int32_t start, int32_t step, int32_t stride, void* stream);
+
 /* Seeded synthetic bytes: out[i] = lo + splitmix64_i(seed) % span (crates/kern-test/src/workload.rs:11-26). */
 int kern_fill_random_u8(void* out, int64_t n, uint64_t seed, int32_t lo, int32_t span, void* stream);
 

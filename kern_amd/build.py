@@ -52,6 +52,15 @@ ENTRIES = {
                                  "out buffer<bf16>", "i32", "i32", "i32", "f32"],
     "kern_mx_moe_finalize": ["in buffer<bf16>", "in buffer<i32>", "in buffer<f32>", "out buffer<bf16>", "i32", "i32",
                              "i32"],
+    "kern_weight_p1_bf16_f32": ["in buffer<bf16>", "out buffer<f32>", "i32"],
+    "kern_cast_bf16_f32": ["in buffer<bf16>", "out buffer<f32>", "i32"],
+    "kern_rope_table_bf16": ["out buffer<bf16>", "out buffer<bf16>", "i32", "i32", "i32", "f32"],
+    "kern_fill_f32": ["out buffer<f32>", "i32", "f32"],
+    "kern_fill_i32": ["out buffer<i32>", "i32", "i32"],
+    "kern_fill_i64": ["out buffer<i64>", "i32", "i64"],
+    "kern_fill_u8": ["out buffer<u8>", "i32", "i32"],
+    "kern_fill_bf16": ["out buffer<bf16>", "i32", "f32"],
+    "kern_iota_i32": ["out buffer<i32>", "i32", "i32", "i32", "i32"],
 }
 
 

@@ -513,6 +513,81 @@ extern "C" int kern_moe_finalize(const void* fc2_out, const int32_t* exp2perm, c
   return launch("kern_mx_moe_finalize", (uint32_t)tokens, 1, 1, 256, stream, a);
 }
 
+// weight_prep family: one thread per element, 256 per workgroup (tools/kernels-src/weight_prep.cu)
+static int elementwise(const char* entry, int32_t n, void* stream, Args& a) {
+  if (n == 0) return KERN_OK;
+  return launch(entry, (uint32_t)((n + 255) / 256), 1, 1, 256, stream, a);
+}
+
+extern "C" int kern_weight_p1_bf16_f32(const void* w, float* out, int32_t n, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || (w && out)), "weight_p1_bf16_f32: need n >= 0 and buffers (n=%d)", n);
+  Args a;
+  a.put(w), a.put(out), a.put(n);
+  return elementwise("kern_weight_p1_bf16_f32", n, stream, a);
+}
+
+extern "C" int kern_cast_bf16_f32(const void* w, float* out, int32_t n, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || (w && out)), "cast_bf16_f32: need n >= 0 and buffers (n=%d)", n);
+  Args a;
+  a.put(w), a.put(out), a.put(n);
+  return elementwise("kern_cast_bf16_f32", n, stream, a);
+}
+
+extern "C" int kern_rope_table_bf16(void* cos_t, void* sin_t, int32_t rows, int32_t half, int32_t stride, float base,
+                                    void* stream) {
+  REQUIRE(rows >= 0 && half > 0 && half <= 1024 && stride >= half && base > 0.f,
+          "rope_table_bf16: need 0 < half <= 1024, stride >= half, base > 0 (rows=%d half=%d stride=%d)", rows, half,
+          stride);
+  if (rows == 0) return KERN_OK;
+  REQUIRE(cos_t && sin_t, "rope_table_bf16: null buffer");
+  Args a;
+  a.put(cos_t), a.put(sin_t), a.put(rows), a.put(half), a.put(stride), a.put(base);
+  return launch("kern_rope_table_bf16", (uint32_t)rows, 1, 1, (uint32_t)((half + 63) / 64 * 64), stream, a);
+}
+
+extern "C" int kern_fill_f32(float* p, int32_t n, float v, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || p), "fill_f32: need n >= 0 and a buffer (n=%d)", n);
+  Args a;
+  a.put(p), a.put(n), a.put(v);
+  return elementwise("kern_fill_f32", n, stream, a);
+}
+
+extern "C" int kern_fill_i32(int32_t* p, int32_t n, int32_t v, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || p), "fill_i32: need n >= 0 and a buffer (n=%d)", n);
+  Args a;
+  a.put(p), a.put(n), a.put(v);
+  return elementwise("kern_fill_i32", n, stream, a);
+}
+
+extern "C" int kern_fill_i64(int64_t* p, int32_t n, int64_t v, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || p), "fill_i64: need n >= 0 and a buffer (n=%d)", n);
+  Args a;
+  a.put(p), a.put(n), a.put(v);
+  return elementwise("kern_fill_i64", n, stream, a);
+}
+
+extern "C" int kern_fill_u8(uint8_t* p, int32_t n, int32_t v, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || p), "fill_u8: need n >= 0 and a buffer (n=%d)", n);
+  Args a;
+  a.put(p), a.put(n), a.put(v);
+  return elementwise("kern_fill_u8", n, stream, a);
+}
+
+extern "C" int kern_fill_bf16(void* p, int32_t n, float v, void* stream) {
+  REQUIRE(n >= 0 && (n == 0 || p), "fill_bf16: need n >= 0 and a buffer (n=%d)", n);
+  Args a;
+  a.put(p), a.put(n), a.put(v);
+  return elementwise("kern_fill_bf16", n, stream, a);
+}
+
+extern "C" int kern_iota_i32(int32_t* p, int32_t n, int32_t start, int32_t step, int32_t stride, void* stream) {
+  REQUIRE(n >= 0 && stride >= 1 && (n == 0 || p), "iota_i32: need n >= 0, stride >= 1 and a buffer (n=%d stride=%d)",
+          n, stride);
+  Args a;
+  a.put(p), a.put(n), a.put(start), a.put(step), a.put(stride);
+  return elementwise("kern_iota_i32", n, stream, a);
+}
+
 extern "C" int kern_fill_random_u8(void* out, int64_t n, uint64_t seed, int32_t lo, int32_t span, void* stream) {
   REQUIRE(n >= 0 && span >= 1 && span <= 256, "fill_random_u8: need n >= 0 and 1 <= span <= 256");
   if (n == 0) return KERN_OK;

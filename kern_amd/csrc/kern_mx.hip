@@ -908,6 +908,67 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize(const uin
   }
 }
 
+// ====================================================================================== weight_prep
+// The derived tables a manifest's `once` program computes after load (tools/kernels-src/weight_prep.cu:1-20).
+// The entry names, argument lists and the one-thread-per-element mapping (i = block * blockDim + thread,
+// nothing past n) are the reference's, so the once-program launches (literal grids) run unchanged.
+
+// out[i] = f32(w[i]) + 1 (GemmaRMSNorm's weight + 1)
+extern "C" __global__ void kern_weight_p1_bf16_f32(const uint16_t* __restrict__ w, float* __restrict__ out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = bf16_bits_to_f32(w[i]) + 1.0f;
+}
+
+// out[i] = f32(w[i])
+extern "C" __global__ void kern_cast_bf16_f32(const uint16_t* __restrict__ w, float* __restrict__ out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = bf16_bits_to_f32(w[i]);
+}
+
+// RoPE cache: inv = 1 / base^(2j / (2 half)), angle = r * inv (f32), cos/sin rounded to bf16 at
+// [r * stride + j] for r < rows, j < half. Grid.x = rows, a thread per column (block >= half).
+extern "C" __global__ void kern_rope_table_bf16(uint16_t* __restrict__ cos_t, uint16_t* __restrict__ sin_t, int rows,
+                                                int half, int stride, float base) {
+  const int j = threadIdx.x, r = blockIdx.x;
+  if (j >= half || r >= rows) return;
+  const float inv = 1.0f / powf(base, (float)(2 * j) / (float)(2 * half));
+  const float angle = (float)r * inv;
+  cos_t[(int64_t)r * stride + j] = (uint16_t)f32_to_bf16_bits(cosf(angle));
+  sin_t[(int64_t)r * stride + j] = (uint16_t)f32_to_bf16_bits(sinf(angle));
+}
+
+extern "C" __global__ void kern_fill_f32(float* __restrict__ p, int n, float v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+extern "C" __global__ void kern_fill_i32(int* __restrict__ p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+extern "C" __global__ void kern_fill_i64(int64_t* __restrict__ p, int n, int64_t v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+extern "C" __global__ void kern_fill_u8(uint8_t* __restrict__ p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = (uint8_t)v;
+}
+
+// the bf16 fill of K3's k3_weight_prep module (fixtures/k3/head.json op fill_bf16): p[i] = bf16(v), RNE
+extern "C" __global__ void kern_fill_bf16(uint16_t* __restrict__ p, int n, float v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+// p[i * stride] = start + i * step
+extern "C" __global__ void kern_iota_i32(int* __restrict__ p, int n, int start, int step, int stride) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[(int64_t)i * stride] = start + i * step;
+}
+
 // ====================================================================================== workload fills
 // Synthetic seeded inputs (splitmix64 stream, crates/kern-test/src/workload.rs:11-26):
 // out[i] = lo + draw_i % span.

@@ -146,6 +146,30 @@ def moe_finalize_rms(H: int, topk: int, eps: float = 1e-6) -> dict:
     }
 
 
+def _fill(entry: str, params: list, launch_params: list, args: list, n: int) -> dict:
+    return {"params": params, "impl": {"launches": [{
+        "module": MODULE, "entry": entry, "params": launch_params, "block": [256, 1, 1],
+        "grid": [_ceil(n, 256), 1, 1], "args": args}]}}
+
+
+def fill_i32(n: int) -> dict:
+    """fill_i32(out i32 p, i32 v): p[0..n) = v (weight_prep.cu kern_fill_i32, n a launch literal)."""
+    return _fill("kern_fill_i32", ["out buffer<i32>", "i32"], ["out buffer<i32>", "i32", "i32"],
+                 [{"param": 0}, {"i32": n}, {"param": 1}], n)
+
+
+def fill_f32(n: int) -> dict:
+    """fill_f32(out f32 p, f32 v): p[0..n) = v."""
+    return _fill("kern_fill_f32", ["out buffer<f32>", "f32"], ["out buffer<f32>", "i32", "f32"],
+                 [{"param": 0}, {"i32": n}, {"param": 1}], n)
+
+
+def fill_bf16(n: int, v: float) -> dict:
+    """fill_bf16(out bf16 p): p[0..n) = bf16(v), v a launch literal (K3's k3_weight_prep kern_fill_bf16)."""
+    return _fill("kern_fill_bf16", ["out buffer<bf16>"], ["out buffer<bf16>", "i32", "f32"],
+                 [{"param": 0}, {"i32": n}, {"f32": v}], n)
+
+
 def moe_ops(H: int, I: int, E: int, topk: int, local_start: int = 0) -> dict:
     """The ops of one MoE layer (hidden H, intermediate I, E local experts, top-k) as `ops` entries."""
     return {

@@ -49,6 +49,15 @@ _SIGS = {
     "kern_mxfp4_gemv_bf16": [P] * 4 + [I32, I32, I32, P],
     "kern_fill_random_u8": [P, I64, ctypes.c_uint64, I32, I32, P],
     "kern_silu_mul": [P, P, I32, I32, P],
+    "kern_weight_p1_bf16_f32": [P, P, I32, P],
+    "kern_cast_bf16_f32": [P, P, I32, P],
+    "kern_rope_table_bf16": [P, P, I32, I32, I32, ctypes.c_float, P],
+    "kern_fill_f32": [P, I32, ctypes.c_float, P],
+    "kern_fill_i32": [P, I32, I32, P],
+    "kern_fill_i64": [P, I32, I64, P],
+    "kern_fill_u8": [P, I32, I32, P],
+    "kern_fill_bf16": [P, I32, ctypes.c_float, P],
+    "kern_iota_i32": [P, I32, I32, I32, I32, P],
     "kern_moe_finalize_rms": [P] * 5 + [I32, I32, I32, ctypes.c_float, P],
     "kern_moe_finalize": [P] * 4 + [I32, I32, I32, P],
     "kern_init": [ctypes.c_char_p],
@@ -237,6 +246,37 @@ def moe_finalize(fc2_out, exp2perm, topk_weight, out, tokens, *, H, topk):
         _ptr(fc2_out, "fc2_out", bf16), _ptr(exp2perm, "exp2perm", i32, tokens * topk),
         _ptr(topk_weight, "topk_weight", f32, tokens * topk), _ptr(out, "out", bf16, tokens * H), tokens, H, topk,
         _stream()))
+
+
+# weight_prep family (tools/kernels-src/weight_prep.cu)
+
+def weight_p1_bf16_f32(w, out):
+    check(lib().kern_weight_p1_bf16_f32(_ptr(w, "w", bf16), _ptr(out, "out", f32, w.numel()), w.numel(), _stream()))
+
+
+def cast_bf16_f32(w, out):
+    check(lib().kern_cast_bf16_f32(_ptr(w, "w", bf16), _ptr(out, "out", f32, w.numel()), w.numel(), _stream()))
+
+
+def rope_table_bf16(cos_t, sin_t, rows, half, stride, base):
+    need = (rows - 1) * stride + half if rows else 0
+    check(lib().kern_rope_table_bf16(_ptr(cos_t, "cos", bf16, need), _ptr(sin_t, "sin", bf16, need), rows, half, stride,
+                                     float(base), _stream()))
+
+
+def fill(p, v):
+    """p[:] = v, by the dtype of p: fill_f32 / fill_i32 / fill_i64 / fill_u8 / fill_bf16."""
+    n = p.numel()
+    fn = {torch.float32: lib().kern_fill_f32, torch.int32: lib().kern_fill_i32, torch.int64: lib().kern_fill_i64,
+          torch.uint8: lib().kern_fill_u8, torch.bfloat16: lib().kern_fill_bf16}.get(p.dtype)
+    if fn is None:
+        raise KernError(4, f"fill: no fill for {p.dtype}")
+    val = float(v) if p.dtype in (torch.float32, torch.bfloat16) else int(v)
+    check(fn(_ptr(p, "p"), n, val, _stream()))
+
+
+def iota_i32(p, n, start=0, step=1, stride=1):
+    check(lib().kern_iota_i32(_ptr(p, "p", i32, (n - 1) * stride + 1 if n else 0), n, start, step, stride, _stream()))
 
 
 def fill_random_u8(out, seed, lo=0, span=256):

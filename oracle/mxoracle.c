@@ -396,6 +396,18 @@ void mxo_moe_finalize(const uint16_t* fc2, const int32_t* e2p, const float* w, c
   free(y);
 }
 
+/* weight_prep's RoPE cache (tools/kernels-src/weight_prep.cu:9-13, :37-47): inv = 1 / base^(2j/(2 half)),
+ * angle = r * inv, all in f32, cos/sin rounded to bf16 at [r*stride + j]. */
+void mxo_rope_table(uint16_t* cos_t, uint16_t* sin_t, int64_t rows, int64_t half, int64_t stride, float base) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t j = 0; j < half; ++j) {
+      float inv = 1.0f / powf(base, (float)(2 * j) / (float)(2 * half));
+      float angle = (float)r * inv;
+      cos_t[r * stride + j] = mxo_f32_to_bf16(cosf(angle));
+      sin_t[r * stride + j] = mxo_f32_to_bf16(sinf(angle));
+    }
+}
+
 /* --------------------------------------------------------------- routing */
 
 int64_t mxo_max_ctas(int64_t tokens, int topk, int experts, int tile) {

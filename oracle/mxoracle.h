@@ -103,6 +103,9 @@ float mxo_situ(float g, float u, float alpha, float beta);
 /* out[t][i] = bf16(bf16(g/(1+exp(-g))) * u), g = in[t][i], u = in[t][d+i]  (tools/kernels-src/silu_mul.cu:1-5) */
 void mxo_silu_mul_bf16(const uint16_t* in, int64_t T, int64_t d, uint16_t* out);
 
+/* RoPE cache of weight_prep.cu: cos/sin[r*stride + j] = bf16(cos/sin(f32(r) * (1 / base^(2j/(2 half))))) */
+void mxo_rope_table(uint16_t* cos_t, uint16_t* sin_t, int64_t rows, int64_t half, int64_t stride, float base);
+
 /* MoE finalize: y[t] = sum_j w[t][j] * fc2[e2p[t*topk+j]] (j ascending, f32 FMAs, e2p < 0 skipped)
  * (tools/trtllm-bmm/probe.py:100-110); gamma == NULL: out = bf16(y), else out = bf16(y / sqrt(mean(y^2) +
  * eps) * gamma) (op moe_finalize_rms; parity unpinned: the reference kernel's source is absent). */

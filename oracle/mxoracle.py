@@ -82,6 +82,7 @@ def _declare(L):
     L.mxo_gemv_w4a16.argtypes = [P, P, P, I64, I64, I64, P, P, I32]
     L.mxo_silu_mul_bf16.argtypes = [P, I64, I64, P]
     L.mxo_moe_finalize.argtypes = [P, P, P, P, I64, I64, I32, ctypes.c_float, P]
+    L.mxo_rope_table.argtypes = [P, P, I64, I64, I64, ctypes.c_float]
     L.mxo_routing.argtypes = [P, I64, I32, I32, I32, I32, P, P, P, P, P, P, P]
     L.mxo_max_ctas.restype = I64
     L.mxo_max_ctas.argtypes = [I64, I32, I32, I32]
@@ -280,6 +281,14 @@ def moe_finalize(fc2_bf16, exp2perm, topk_weight, gamma_bf16, T, H, topk, eps=0.
     out = np.empty((T, H), np.uint16)
     lib().mxo_moe_finalize(_p(fc2), _p(e2p), _p(w), None if g is None else _p(g), T, H, topk, float(eps), _p(out))
     return out
+
+
+def rope_table(rows, half, stride, base):
+    """weight_prep's RoPE cache -> (cos, sin) bf16 bits, each [rows * stride] (unwritten columns zero)."""
+    c = np.zeros(rows * stride, np.uint16)
+    s_ = np.zeros(rows * stride, np.uint16)
+    lib().mxo_rope_table(_p(c), _p(s_), rows, half, stride, float(base))
+    return c, s_
 
 
 def max_ctas(tokens, topk, experts, tile=128):

@@ -8,7 +8,8 @@ import json
 import os
 import sys
 
-OPS = ["moe_quant", "k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_routing", "moe_fc1", "moe_fc2", "moe_finalize_rms"]
+OPS = ["moe_quant", "k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_routing", "moe_fc1", "moe_fc2", "moe_finalize_rms",
+       "fill_i32", "fill_f32", "fill_bf16"]
 
 
 def main(ref):
@@ -21,6 +22,10 @@ def main(ref):
         rec = {"params": op["params"]}
         if name in ("k3_moe_w_shuffle", "k3_moe_sf_shuffle", "moe_fc1", "moe_fc2", "moe_finalize_rms"):
             rec["grid"] = op["impl"]["launches"][0]["grid"]
+        if name.startswith("fill_"):  # the kernel ABI and the literal args of the once-program launch
+            launch = op["impl"]["launches"][0]
+            rec.update({"entry": launch["entry"], "launch_params": launch["params"], "args": launch["args"],
+                        "grid": launch["grid"], "block": launch["block"]})
         out["ops"][name] = rec
     dst = os.path.join(os.path.dirname(os.path.abspath(__file__)), "k3_op_interfaces.json")
     with open(dst, "w") as f:

