@@ -30,6 +30,8 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
   to MXFP8 and takes the GEMM; the O input stands in for attention (out of scope); the O output feeds
   the layer's MoE and the finalized MoE output the next layer. Reported per M: step time, algorithmic HBM bytes (weights touched +
   activations) as GB/s and FLOPs as TFLOP/s.
+* `mxfp8_dense` = extern:cublaslt_mxfp8_tn's analog at config 3's shape with MXFP8 weights: [4096, 7168] x
+  [2048, 7168]^T, bf16 out; TFLOP/s against the dense FP8 MFMA peak.
 * `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on a bounded
   sample of the same GEMM (its first rows), in the headline unit.
 * `traffic` comes from committed rocprofv3 --pmc summaries (profiles/traffic.json), null without one.
@@ -68,7 +70,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["gemm", "decode", "moe", "stack", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "decode", "moe", "stack", "mxfp8", "copy"], default=None,
                     help="run one leg only (for profiling); the JSON line then carries that leg. 'copy' runs "
                          "three plain 256 MiB device copies: the reference for scaling HBM byte counters")
     ap.add_argument("--decode-m", type=int, default=1)
@@ -386,6 +388,40 @@ def bench_stack(torch, ops, wl, stream, steps, warmup):
     return res
 
 
+def bench_mxfp8(torch, ops, wl, stream, steps, warmup):
+    """extern:cublaslt_mxfp8_tn analog at config 3's shape, MXFP8 operands on both sides."""
+    u8 = torch.uint8
+    M, N, K = PM, PN, PK
+    log(f"mxfp8 dense: M={M} N={N} K={K}")
+    x = dev_from_np(wl.activations_bf16(7, M, K), torch)
+    wb = dev_from_np(wl.activations_bf16(8, N, K), torch)
+    qa, sa = ops.quantize_mxfp8(x)
+    qw, sw = ops.quantize_mxfp8(wb)
+    # scales into the 128x4 tiled layout the op takes (a load-time relayout, outside the timed loop)
+    import numpy as np
+
+    def tiled(sf, rows):
+        kb = K // 32
+        r = np.arange(rows)[:, None]
+        b = np.arange(kb)[None, :]
+        off = (r // 128 * -(-kb // 4) + b // 4) * 512 + r % 32 * 16 + r % 128 // 32 * 4 + b % 4
+        t = np.full(ops.r128c4_bytes(rows, kb), 127, np.uint8)
+        t[off] = sf.cpu().numpy()
+        return torch.from_numpy(t).cuda()
+
+    ta, tw = tiled(sa, M), tiled(sw, N)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    ms, _ = timed_loop(torch, stream, lambda i: ops.cublaslt_mxfp8_tn(qa, qw, c, ta, tw, M, N, K), steps, warmup)
+    flop = 2.0 * M * N * K
+    t = flop / (ms * 1e-3) / 1e12
+    return {"metric": "MXFP8 x MXFP8 dense GEMM TFLOP/s", "value": round(t, 1), "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(t, 1), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(t / PEAK_FP8_TFLOPS, 4), "traffic": load_traffic("kern_mx_gemm_mxfp8"),
+                         "kernel": "kern_mx_gemm_mxfp8", "kernel_us": round(ms * 1e3, 3), "algorithmic_flop": flop},
+            "config": {"M": M, "N": N, "K": K}}
+
+
 def cpu_baseline_gemm(torch, wl, tensors):
     """The C oracle on the first rows of the same GEMM (bounded sample), fp32 accumulation."""
     import numpy as np
@@ -447,6 +483,10 @@ def main():
         st = None
         if args.only in (None, "stack"):
             st = bench_stack(torch, ops, wl, stream, args.steps, args.warmup)
+        torch.cuda.synchronize()
+        m8 = None
+        if args.only in (None, "mxfp8"):
+            m8 = bench_mxfp8(torch, ops, wl, stream, args.steps, args.warmup)
     torch.cuda.synchronize()
 
     cpu = None
@@ -508,8 +548,13 @@ def main():
             "decode": dec,
             "moe": moe,
             "stack": None if st is None else {"metric": "config 5 layer stack (4 layers, hipGraph)", **st},
+            "mxfp8_dense": m8,
             "cpu_baseline": cpu,
         }
+    elif m8 is not None and st is None and dec is None and moe is None:
+        out = dict(m8)
+        out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+                    "scaling": "weak", "vs_baseline": None, "dtype": "mxfp8xmxfp8->f32", "data": "synthetic"})
     elif st is not None and dec is None and moe is None:
         out = {"metric": "config 5 layer stack (4 layers, hipGraph)", **st}
         out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

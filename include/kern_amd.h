@@ -208,6 +208,13 @@ int kern_mxfp4_gemm_bf16(const void* a, const void* sf_a, const void* b, const v
 int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_sf, void* y, int32_t M, int32_t N, int32_t K,
                          void* stream);
 
+/* extern:cublaslt_mxfp8_tn (crates/kern-runtime/src/cublas.rs:387-400; args [a, w, c, a_scale, w_scale, m,
+ * n, k, ldc]): c bf16 [m][ldc] = sum_k deq(a)[m][k] * deq(w)[n][k], a [m][k] and w [n][k] e4m3, scales
+ * e8m0 per 32 of K in the 128x4 tiled layout (rows padded to 128, k blocks to 4). k % 32 == 0,
+ * ldc >= n, operands below 2 GiB. f32 accumulation, bf16 RNE out. */
+int kern_mxfp8_gemm_bf16(const void* a, const void* w, void* c, const void* a_sf, const void* w_sf, int32_t m,
+                         int32_t n, int32_t k, int32_t ldc, void* stream);
+
 /* silu_mul (tools/kernels-src/silu_mul.cu:1-36, kernel ABI (out, in, d), grid [tokens, ceil(d/2048)]):
  * out bf16 [tokens][d] = bf16(bf16(g / (1 + exp(-g))) * u), g = in[t][i], u = in[t][d + i], in bf16
  * [tokens][2d]. d % 8 == 0. */

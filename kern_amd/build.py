@@ -61,6 +61,8 @@ ENTRIES = {
     "kern_fill_u8": ["out buffer<u8>", "i32", "i32"],
     "kern_fill_bf16": ["out buffer<bf16>", "i32", "f32"],
     "kern_iota_i32": ["out buffer<i32>", "i32", "i32", "i32", "i32"],
+    "kern_mx_gemm_mxfp8": ["in buffer<fp8e4m3>", "in buffer<fp8e4m3>", "out buffer<bf16>", "in buffer<u8>",
+                           "in buffer<u8>", "i32", "i32", "i32", "i32"],
 }
 
 

@@ -513,6 +513,20 @@ extern "C" int kern_moe_finalize(const void* fc2_out, const int32_t* exp2perm, c
   return launch("kern_mx_moe_finalize", (uint32_t)tokens, 1, 1, 256, stream, a);
 }
 
+extern "C" int kern_mxfp8_gemm_bf16(const void* a, const void* w, void* c, const void* a_sf, const void* w_sf, int32_t m,
+                                    int32_t n, int32_t k, int32_t ldc, void* stream) {
+  REQUIRE(m >= 0 && n >= 0 && k >= 0 && k % 32 == 0 && ldc >= n,
+          "cublaslt_mxfp8_tn: need k %% 32 == 0 and ldc >= n (m=%d n=%d k=%d ldc=%d)", m, n, k, ldc);
+  if (m == 0 || n == 0) return KERN_OK;
+  REQUIRE((int64_t)m * k < ((int64_t)1 << 31) && (int64_t)n * k < ((int64_t)1 << 31) && (m + 127) / 128 <= 65535,
+          "cublaslt_mxfp8_tn: operands beyond 2 GiB or m beyond the grid (m=%d n=%d k=%d)", m, n, k);
+  REQUIRE(a && w && c && a_sf && w_sf, "cublaslt_mxfp8_tn: null buffer");
+  if (k == 0) return fail(KERN_ERR_API, "cublaslt_mxfp8_tn: k == 0 leaves c undefined; zero it instead");
+  Args x;
+  x.put(a), x.put(w), x.put(c), x.put(a_sf), x.put(w_sf), x.put(m), x.put(n), x.put(k), x.put(ldc);
+  return launch("kern_mx_gemm_mxfp8", (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 1, 256, stream, x);
+}
+
 // weight_prep family: one thread per element, 256 per workgroup (tools/kernels-src/weight_prep.cu)
 static int elementwise(const char* entry, int32_t n, void* stream, Args& a) {
   if (n == 0) return KERN_OK;

@@ -705,6 +705,148 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_bf16(const uint8_
   bmm_tile<MODE_DENSE_BF16>(A, L);
 }
 
+// ====================================================================================== MXFP8 x MXFP8 GEMM
+// extern:cublaslt_mxfp8_tn (crates/kern-runtime/src/cublas.rs:387-400): row-major C[m][n] (bf16, row stride
+// ldc) = sum_k deq(A)[m][k] * deq(W)[n][k]; A [m][k] and W [n][k] e4m3, each with an e8m0 scale per 32
+// elements of K in the 128x4 tiled layout (rows padded to 128, k blocks to 4; block (r/128, b/4) at
+// 512 (r/128 * ceil(K/128) + b/4), entry (r, b) at (r%32)*16 + (r%128/32)*4 + b%4). K % 32 == 0.
+//
+// One workgroup of 4 waves computes a 128 (m) x 128 (n) tile, wave (wm, wn) = 64 x 64, on
+// V_MFMA_SCALE_F32_16X16X128_F8F6F4 with W as the A operand and A as the B operand (so each lane ends
+// with four consecutive n of one m). Both operands go from memory straight into LDS (buffer loads: reads
+// past an operand's end return zeros; rows past m or n read the last valid row and are never stored),
+// 16-byte chunk j of row t at t*128 + ((j ^ ((t>>1)&7)) << 4), double-buffered over 128-wide k-tiles.
+// Each k-tile's two 512-byte scale blocks are staged alongside. In the last k-tile, when K % 128 != 0,
+// the chunks past K are zeroed in registers and the scale bytes of k blocks past K read as 1.0.
+#define G8_LDS_T 16384  // one operand tile: 128 rows x 128 B
+#define G8_LDS_STAGE (2 * G8_LDS_T + 1024)
+
+extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_mxfp8(const uint8_t* __restrict__ a,
+                                                                     const uint8_t* __restrict__ w,
+                                                                     uint16_t* __restrict__ c,
+                                                                     const uint8_t* __restrict__ a_sf,
+                                                                     const uint8_t* __restrict__ w_sf, int M, int N,
+                                                                     int K, int ldc) {
+  __shared__ __attribute__((aligned(1024))) uint8_t st0[G8_LDS_STAGE], st1[G8_LDS_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * 128, n0 = blockIdx.x * 128;
+  const int KT = (K + 127) >> 7, KB = K >> 5, kb4 = (KB + 3) >> 2;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)a, (short)0, M * K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, N * K, 0x00020000);
+  const int mt = (M + 127) >> 7, nt = (N + 127) >> 7;
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)a_sf, (short)0, mt * kb4 * 512, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)w_sf, (short)0, nt * kb4 * 512, 0x00020000);
+  // this lane's source rows and 16-byte chunk for request r (rows 32r + 8*wave + lane/8)
+  int offa[4], offw[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = 32 * r + 8 * wave + (lane >> 3);
+    const int chunk = ((lane & 7) ^ ((t >> 1) & 7)) << 4;
+    offa[r] = min(m0 + t, M - 1) * K + chunk;
+    offw[r] = min(n0 + t, N - 1) * K + chunk;
+  }
+  // scale blocks: waves 0-1 bring the two halves of A's block, waves 2-3 W's
+  const __amdgpu_buffer_rsrc_t rs = wave < 2 ? rsa : rsw;
+  const int sbase = (wave < 2 ? blockIdx.y : blockIdx.x) * kb4 * 512 + (wave & 1) * 256 + lane * 4;
+  auto dma_tile = [&](int kt, uint8_t* stg) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stg + (r * 4 + wave) * 1024), 16, offa[r] + kt * 128, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(stg + G8_LDS_T + (r * 4 + wave) * 1024), 16,
+                                               offw[r] + kt * 128, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(stg + 2 * G8_LDS_T + (wave >> 1) * 512 + (wave & 1) * 256),
+                                             4, sbase + kt * 512, 0, 0, 0);
+  };
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  const int cl = lane & 15, g = lane >> 4;
+
+  auto tile = [&](const uint8_t* stg, bool last) {
+    // operands: n subtiles (A operand, from W) and m subtiles (B operand, from A)
+    v8i wo[4], ao[4];
+    uint32_t sw_[4], sa_[4];
+    const int kr = K & 127;  // valid bytes of a partial last tile
+    const bool v0 = !last || kr == 0 || 16 * g < kr, v1 = !last || kr == 0 || 64 + 16 * g < kr;
+    const bool vs = !last || kr == 0 || 32 * g < kr;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      {
+        const int t = wn * 64 + q * 16 + cl;
+        const uint8_t* row = stg + G8_LDS_T + t * 128;
+        const int sw = (t >> 1) & 7;
+        v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
+        v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
+        if (!v0) x0 = (v4i){0, 0, 0, 0};
+        if (!v1) x1 = (v4i){0, 0, 0, 0};
+        wo[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        sw_[q] = vs ? stg[2 * G8_LDS_T + 512 + (t & 31) * 16 + (t >> 5) * 4 + g] : 127u;
+      }
+      {
+        const int t = wm * 64 + q * 16 + cl;
+        const uint8_t* row = stg + t * 128;
+        const int sw = (t >> 1) & 7;
+        v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
+        v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
+        if (!v0) x0 = (v4i){0, 0, 0, 0};
+        if (!v1) x1 = (v4i){0, 0, 0, 0};
+        ao[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        sa_[q] = vs ? stg[2 * G8_LDS_T + (t & 31) * 16 + (t >> 5) * 4 + g] : 127u;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wo[j], ao[i], acc[i][j], 0, 0, 0, (int)sw_[j], 0,
+                                                                      (int)sa_[i]);
+  };
+
+  dma_tile(0, st0);
+  for (int kt = 0; kt < KT; ++kt) {
+    uint8_t* cur = (kt & 1) ? st1 : st0;
+    uint8_t* nxt = (kt & 1) ? st0 : st1;
+    const bool more = kt + 1 < KT;
+    if (more) {
+      dma_tile(kt + 1, nxt);
+      WAIT_VMCNT(9);  // tile kt has landed for this wave (tile kt+1's nine requests may be in flight)
+    } else {
+      WAIT_VMCNT(0);
+    }
+    __syncthreads();  // ... and for every wave
+    tile(cur, !more);
+    __syncthreads();  // every read of `cur` is done before tile kt+2 lands in it
+  }
+
+  // lane (cl, g) of tile (i, j) holds n = n0 + wn*64 + 16j + 4g + (0..3) for m = m0 + wm*64 + 16i + cl
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wm * 64 + 16 * i + cl;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 64 + 16 * j + 4 * g;
+      const v4f v = acc[i][j];
+      uint16_t* dst = c + (int64_t)m * ldc + n;
+      if (n + 3 < N && ((((uintptr_t)dst) & 7) == 0)) {
+        const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) dst[e] = (uint16_t)f32_to_bf16_bits(v[e]);
+      }
+    }
+  }
+}
+
 // ====================================================================================== routing
 // op moe_routing (head.json:25117): in i32 topk_idx[T][topk]; out counts [2E], cta_batch, cta_limit,
 // num_non_exiting[1], total_padded[1], route_map, exp2perm [T*topk]; launch adds i32 T, i32 topk,

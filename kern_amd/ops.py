@@ -49,6 +49,7 @@ _SIGS = {
     "kern_mxfp4_gemv_bf16": [P] * 4 + [I32, I32, I32, P],
     "kern_fill_random_u8": [P, I64, ctypes.c_uint64, I32, I32, P],
     "kern_silu_mul": [P, P, I32, I32, P],
+    "kern_mxfp8_gemm_bf16": [P] * 5 + [I32, I32, I32, I32, P],
     "kern_weight_p1_bf16_f32": [P, P, I32, P],
     "kern_cast_bf16_f32": [P, P, I32, P],
     "kern_rope_table_bf16": [P, P, I32, I32, I32, ctypes.c_float, P],
@@ -223,6 +224,20 @@ def mxfp4_gemv_bf16(x, w, w_sf, y, M, *, N, K):
     check(lib().kern_mxfp4_gemv_bf16(
         _ptr(x, "x", bf16, M * K), _ptr(w, "w", u8, N * K // 2), _ptr(w_sf, "w_sf", u8, N * K // 32),
         _ptr(y, "y", bf16, M * N), M, N, K, _stream()))
+
+
+def r128c4_bytes(rows, kblocks):
+    """Bytes of the 128x4 tiled scale layout: rows padded to 128, k blocks to 4 (cublas.rs:396-400)."""
+    return -(-rows // 128) * 512 * -(-kblocks // 4)
+
+
+def cublaslt_mxfp8_tn(a, w, c, a_sf, w_sf, m, n, k, ldc=None):
+    """extern:cublaslt_mxfp8_tn: c bf16 [m, ldc] = MXFP8 a [m, k] x MXFP8 w [n, k]^T, scales 128x4-tiled."""
+    ldc = n if ldc is None else ldc
+    check(lib().kern_mxfp8_gemm_bf16(
+        _ptr(a, "a", u8, m * k), _ptr(w, "w", u8, n * k), _ptr(c, "c", bf16, (m - 1) * ldc + n if m else 0),
+        _ptr(a_sf, "a_sf", u8, r128c4_bytes(m, k // 32)), _ptr(w_sf, "w_sf", u8, r128c4_bytes(n, k // 32)),
+        m, n, k, ldc, _stream()))
 
 
 def silu_mul(out, x, tokens, d):

@@ -408,6 +408,12 @@ void mxo_rope_table(uint16_t* cos_t, uint16_t* sin_t, int64_t rows, int64_t half
     }
 }
 
+/* Linear [rows][kblocks] e8m0 scales from the 128x4 tiled layout (mxo_r128c4_offset). */
+void mxo_r128c4_gather(const uint8_t* tiled, int64_t rows, int64_t kblocks, uint8_t* linear) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t b = 0; b < kblocks; ++b) linear[r * kblocks + b] = tiled[mxo_r128c4_offset(r, b, kblocks)];
+}
+
 /* --------------------------------------------------------------- routing */
 
 int64_t mxo_max_ctas(int64_t tokens, int topk, int experts, int tile) {

@@ -103,6 +103,9 @@ float mxo_situ(float g, float u, float alpha, float beta);
 /* out[t][i] = bf16(bf16(g/(1+exp(-g))) * u), g = in[t][i], u = in[t][d+i]  (tools/kernels-src/silu_mul.cu:1-5) */
 void mxo_silu_mul_bf16(const uint16_t* in, int64_t T, int64_t d, uint16_t* out);
 
+/* Linear [rows][kblocks] scales gathered from the 128x4 tiled layout (cublas.rs:396-400). */
+void mxo_r128c4_gather(const uint8_t* tiled, int64_t rows, int64_t kblocks, uint8_t* linear);
+
 /* RoPE cache of weight_prep.cu: cos/sin[r*stride + j] = bf16(cos/sin(f32(r) * (1 / base^(2j/(2 half))))) */
 void mxo_rope_table(uint16_t* cos_t, uint16_t* sin_t, int64_t rows, int64_t half, int64_t stride, float base);
 

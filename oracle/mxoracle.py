@@ -83,6 +83,7 @@ def _declare(L):
     L.mxo_silu_mul_bf16.argtypes = [P, I64, I64, P]
     L.mxo_moe_finalize.argtypes = [P, P, P, P, I64, I64, I32, ctypes.c_float, P]
     L.mxo_rope_table.argtypes = [P, P, I64, I64, I64, ctypes.c_float]
+    L.mxo_r128c4_gather.argtypes = [P, I64, I64, P]
     L.mxo_routing.argtypes = [P, I64, I32, I32, I32, I32, P, P, P, P, P, P, P]
     L.mxo_max_ctas.restype = I64
     L.mxo_max_ctas.argtypes = [I64, I32, I32, I32]
@@ -248,6 +249,22 @@ def gemm_f32(X, W, nthreads=None):
     C = np.empty((T, N), np.float32)
     lib().mxo_gemm_f32(_p(X), _p(W), T, N, K, _p(C), nthreads or nthreads_default())
     return C
+
+
+def r128c4_gather(tiled, rows, kblocks):
+    """Linear [rows, kblocks] scales from the 128x4 tiled layout."""
+    t = _c(tiled, np.uint8)
+    out = np.empty((rows, kblocks), np.uint8)
+    lib().mxo_r128c4_gather(_p(t), rows, kblocks, _p(out))
+    return out
+
+
+def mxfp8_gemm(a, w, a_sf_tiled, w_sf_tiled, m, n, k, nthreads=None):
+    """extern:cublaslt_mxfp8_tn on the CPU: f32 C [m, n] = deq(a) [m, k] x deq(w) [n, k]^T, f32 accumulation
+    over exactly dequantised operands (scales in the 128x4 tiled layout)."""
+    A = deq_fp8(a, r128c4_gather(a_sf_tiled, m, k // 32), m, k)
+    W = deq_fp8(w, r128c4_gather(w_sf_tiled, n, k // 32), n, k)
+    return gemm_f32(A, W, nthreads)
 
 
 def gemv_w4a16(x_bf16, w_raw, sf_raw, nthreads=None):

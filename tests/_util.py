@@ -46,3 +46,31 @@ def r128c4_offsets(rows, kblocks):
     b = np.arange(kblocks)[None, :]
     kb4 = (kblocks + 3) // 4
     return 512 * ((r // 128) * kb4 + b // 4) + (r % 32) * 16 + ((r % 128) // 32) * 4 + b % 4
+
+
+def mxfp8_kat(shift=0):
+    """The closed-form case of crates/kern-runtime/tests/mxfp8_gemm.rs:9-95: A row i holds one 1.0 at column
+    7i mod K, W[n][k] = ((n + k) % 5) - 2, e8m0 exponents ea(r, b), ew(r, b) (+ shift on W), tiled 128x4;
+    out[i][n] = W[n][col(i)] * 2^(ea(i, b) + ew(n, b) + shift), exact in bf16."""
+    M, N, K = 256, 160, 320
+    KB = K // 32
+    code = {0.0: 0x00, 1.0: 0x38, 2.0: 0x40, -1.0: 0xB8, -2.0: 0xC0}
+    col = lambda i: i * 7 % K
+    a = np.zeros((M, K), np.uint8)
+    for i in range(M):
+        a[i, col(i)] = code[1.0]
+    wv = lambda n, k: float((n + k) % 5 - 2)
+    w = np.array([[code[wv(n, k)] for k in range(K)] for n in range(N)], np.uint8)
+    ea = lambda r, b: (r + b) % 3 - 1
+    ew = lambda r, b: (3 * r + 2 * b) % 5 - 2 + shift
+
+    def tiled(rows, e):
+        kb4, sf = -(-KB // 4), np.full(-(-rows // 128) * -(-KB // 4) * 512, 127, np.uint8)
+        for r in range(rows):
+            for b in range(KB):
+                sf[(r // 128 * kb4 + b // 4) * 512 + r % 32 * 16 + r % 128 // 32 * 4 + b % 4] = 127 + e(r, b)
+        return sf
+
+    want = np.array([[wv(n, col(i)) * 2.0 ** (ea(i, col(i) // 32) + ew(n, col(i) // 32)) for n in range(N)]
+                     for i in range(M)], np.float32)
+    return dict(M=M, N=N, K=K, a=a, w=w, a_sf=tiled(M, ea), w_sf=tiled(N, ew), want=want)

@@ -135,3 +135,14 @@ def test_k3_fills_through_manifest_ops(ops):
     assert p_i.tolist() == [42] + [-1] * 7
     assert (p_f[:224] == -0.75).all() and (p_f[224:] == 0).all()
     assert p_b.float().tolist() == [1.0, 0.0, 0.0, 0.0]
+
+
+def test_mxfp8_kat_through_manifest_op(ops):
+    from tests._util import mxfp8_kat
+    c = mxfp8_kat(0)
+    M, N, K = c["M"], c["N"], c["K"]
+    out = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+    op = ops.ManifestOp(mf.cublaslt_mxfp8_tn(N))
+    op(*(_dev(c[x]) for x in ("a", "w")), out, *(_dev(c[x]) for x in ("a_sf", "w_sf")), M, N, K, vars={"tokens": M})
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), wl.f32_to_bf16_bits(c["want"]))

@@ -399,3 +399,50 @@ def test_rope_table(ops, oracle, rows, half, stride, base):
         g, r = wl.bf16_bits_to_f32(got).astype(np.float64), wl.bf16_bits_to_f32(ref).astype(np.float64)
         assert (np.abs(g - r) <= 2.0**-7 * np.abs(r) + 4 * 2.0**-23 * ang + 1e-6).all()  # ulp <= 2^-7 |x|
         assert (got == ref).mean() > 0.99
+
+
+# --------------------------------------------------------------------------------------- MXFP8 x MXFP8
+
+def test_mxfp8_gemm_kat(ops):
+    from tests._util import mxfp8_kat
+    c = mxfp8_kat(0)
+    M, N, K = c["M"], c["N"], c["K"]
+    a, w, a_sf, w_sf = (to_dev(c[x]) for x in ("a", "w", "a_sf", "w_sf"))
+    out = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+    ops.cublaslt_mxfp8_tn(a, w, out, a_sf, w_sf, M, N, K)
+    _sync()
+    np.testing.assert_array_equal(to_np(out), wl.f32_to_bf16_bits(c["want"]))
+    # captured once, replayed after the scales change on the device: they are read at run time
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with ops.Graph() as g:
+            ops.cublaslt_mxfp8_tn(a, w, out, a_sf, w_sf, M, N, K)
+        w_sf.copy_(to_dev(mxfp8_kat(-1)["w_sf"]))
+        out.zero_()
+        g.launch()
+    _sync()
+    np.testing.assert_array_equal(to_np(out), wl.f32_to_bf16_bits(mxfp8_kat(-1)["want"]))
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 520, 1024), (64, 1000, 2080), (200, 256, 96), (2048, 2048, 7168)])
+def test_mxfp8_gemm_random(ops, oracle, m, n, k):
+    from kern_amd import ops as o
+    rng = np.random.default_rng(m + n + k)
+    xa = wl.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    xw = wl.f32_to_bf16_bits(rng.standard_normal((n, k)).astype(np.float32))
+    qa, sa = oracle.quant_mxfp8(xa)
+    qw, sw = oracle.quant_mxfp8(xw)
+
+    def tiled(sf, rows):
+        t = np.full(o.r128c4_bytes(rows, k // 32), 127, np.uint8)
+        t[r128c4_offsets(rows, k // 32)] = sf
+        return t
+
+    ta, tw = tiled(sa, m), tiled(sw, n)
+    out = torch.zeros((m, n + 8), dtype=torch.bfloat16, device="cuda")  # ldc = n + 8: the gap stays zero
+    ops.cublaslt_mxfp8_tn(to_dev(qa), to_dev(qw), out, to_dev(ta), to_dev(tw), m, n, k, ldc=n + 8)
+    _sync()
+    got = bf16_to_f32(to_np(out))
+    assert not got[:, n:].any()
+    ref = oracle.mxfp8_gemm(qa, qw, ta, tw, m, n, k)
+    assert_gemm_close(got[:, :n], ref, f"mxfp8 {m}x{n}x{k}")

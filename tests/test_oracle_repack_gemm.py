@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from kern_amd import workload as wl
-from tests._util import assert_gemm_close, r128c4_offsets
+from tests._util import assert_gemm_close, r128c4_offsets, mxfp8_kat
 
 
 @pytest.mark.parametrize("gated", [0, 1])
@@ -183,3 +183,12 @@ def test_fc1_oracle_gated_pairs(oracle):
             np.testing.assert_array_equal(c[p], qq[0])
             for b in range(half // 32):
                 assert sf_c[oracle.r128c4_offset(p, b, half // 32)] == sref[0, b]
+
+
+# ---------------------------------------------------------------- MXFP8 x MXFP8 (extern:cublaslt_mxfp8_tn)
+
+@pytest.mark.parametrize("shift", [0, -1])
+def test_mxfp8_gemm_oracle_kat(oracle, shift):
+    c = mxfp8_kat(shift)
+    got = oracle.mxfp8_gemm(c["a"], c["w"], c["a_sf"], c["w_sf"], c["M"], c["N"], c["K"])
+    np.testing.assert_array_equal(got, c["want"])
