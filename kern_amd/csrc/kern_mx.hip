@@ -253,6 +253,8 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 //      applied on the global side, each lane fetching the chunk that belongs at its LDS position;
 //   scales once per 512 of K (two slots): W fragments verbatim, X as dwords [k-tile][row].
 enum { MODE_FC2 = 0, MODE_FC1 = 1, MODE_PT = 2, MODE_DENSE_BF16 = 3 };
+// MoE slots with at most this many rows (one 16-row token subtile) run on the skinny kernels
+#define SKINNY_ROWS 16
 
 struct BmmArgs {
   const uint8_t* a;      // repacked weights [E][m][k/2]
@@ -299,6 +301,147 @@ struct BmmLds {
   uint8_t* sx[2];
 };
 
+// The tile's epilogue (every mode): lane (c, g) of accumulator (ts, rs) of wave (wt, wn) holds weight
+// rows nx*BN + wn*64 + 16*rs + 4*g + i for tile row wt*64 + 16*ts + c; rows at or past `valid` are not
+// stored.
+template <int MODE>
+KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int wn, int nx, int row0, int valid,
+                           int expert, int lane) {
+  const int m = A.m;
+  const int c = lane & 15, g = lane >> 4;
+  const int wrow0 = nx * BN + wn * 64;  // first weight row of this wave
+  if (MODE == MODE_FC2 || MODE == MODE_DENSE_BF16) {
+    uint16_t* C = reinterpret_cast<uint16_t*>(A.c);
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const int t = wt * 64 + ts * 16 + c;
+      if (t < valid) {
+        const int64_t p = row0 + t;
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs) {
+          const int n = wrow0 + rs * 16 + g * 4;
+          const v4f v = acc[ts][rs];
+          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
+          uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+          uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+          *reinterpret_cast<uint2*>(C + p * m + n) = make_uint2(lo, hi);
+        }
+      }
+    }
+  } else if (MODE == MODE_PT) {
+    uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
+    const float ds = A.d_scale[0];
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const int t = wt * 64 + ts * 16 + c;
+      if (t < valid) {
+        const int64_t p = row0 + t;
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs) {
+          const int n = wrow0 + rs * 16 + g * 4;
+          const v4f v = acc[ts][rs];
+          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
+          const uint32_t o = e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
+          *reinterpret_cast<uint32_t*>(C + p * m + n) = o;
+        }
+      }
+    }
+  } else {  // MODE_FC1: gated SiTU-GLU, e4m3 + ue8m0 block-32 (R128c4) output
+    uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
+    const int half = m >> 1;
+    const float al = A.alpha[expert], be = A.beta[expert];
+    // the wave's 64 interleaved gate/up rows give 32 output columns: one MXFP8 block
+    const int ncol0 = (nx * BN + wn * 64) >> 1;
+    const int blk = ncol0 >> 5;
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      const int t = wt * 64 + ts * 16 + c;
+      // h for 4 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
+      float h[4][2];
+#pragma unroll
+      for (int rs = 0; rs < 4; ++rs) {
+        const v4f v = acc[ts][rs];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float gg = v[i], uu = v[i + 2];
+          const float sg = 1.0f / (1.0f + __expf(-gg));
+          h[rs][i] = al * tanhf(gg / al) * sg * be * tanhf(uu / be);
+        }
+      }
+      const bool ok = t < valid;
+      const int64_t p = row0 + t;
+      if (ok && A.dbg) {
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int n = ncol0 + 8 * rs + 2 * g + i;
+            A.dbg[(p * 3 + 0) * half + n] = acc[ts][rs][i];
+            A.dbg[(p * 3 + 1) * half + n] = acc[ts][rs][i + 2];
+            A.dbg[(p * 3 + 2) * half + n] = h[rs][i];
+          }
+      }
+      uint32_t amax = 0;
+#pragma unroll
+      for (int rs = 0; rs < 4; ++rs)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[rs][i]) & 0x7fffffffu);
+      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
+      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
+      const uint32_t sc = mx_scale_code(amax);
+      if (ok) {
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs) {
+          const int n = ncol0 + 8 * rs + 2 * g;
+          const uint32_t o = mx_code2(h[rs][0], h[rs][1], sc);
+          *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
+        }
+        if (g == 0) {
+          const int64_t kb4 = ((half >> 5) + 3) >> 2;
+          const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
+          A.sf_c[off] = (uint8_t)sc;
+        }
+      }
+    }
+  }
+}
+
+// Workgroup -> (weight tile nx of gx, token slot). The hardware hands workgroups to the 8 XCDs round robin
+// (workgroup lin = x + gridDim.x * y to XCD lin % 8), each XCD with its own L2.
+// MoE grids (slot-major, only a prefix of the slots live, the rest exit at once): slot s runs on XCD s % 8
+// with its gx weight tiles back to back, so the live prefix spreads evenly over all XCDs and a slot's
+// activation tile is shared within one L2; a bijection when gridDim.y % 8 == 0 (the host rounds the slot
+// bound up to that). Dense grids (every tile live): each XCD takes a contiguous run of tiles.
+template <bool MOE>
+KERN_DEV void tile_of(int gx, int& nx, int& slot) {
+  const int total = gridDim.x * gridDim.y;
+  int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  if (MOE && (gridDim.y & 7) == 0) {
+    const int j = lin >> 3;
+    nx = j % gx;
+    slot = (j / gx) * 8 + (lin & 7);
+    return;
+  }
+  if (!MOE && (total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  nx = lin % gx;
+  slot = lin / gx;
+}
+
+// Whether an MoE launch runs its small slots (at most SKINNY_ROWS rows) on the skinny kernel: when every
+// slot of an 8-slot sample spread over the live ones is small, as in decode-sized batches. Otherwise the
+// LDS-ring kernel takes every slot: split, the two launches' tails add up, which costs more than the
+// ring's overhead on the small slots. Every workgroup of both kernels reads the same sample, so the two
+// kernels agree on every slot.
+KERN_DEV bool skinny_batch(const int* cta_limit, int live) {
+  bool small = true;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int s = (i * live) >> 3;
+    small = small && cta_limit[s] - s * BT <= SKINNY_ROWS;
+  }
+  return small;
+}
+
 template <int MODE>
 KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   // the wave index through readfirstlane: provably uniform, so everything derived from it (the LDS
@@ -306,12 +449,8 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wt = wave >> 2, wn = wave & 3;  // token half, weight quarter
   const int gx = A.m / BN;
-  // XCD-aware linearisation: consecutive workgroups land on different XCDs (round robin over 8); give
-  // each XCD a contiguous run of tiles so that its L2 sees the reuse.
-  const int total = gridDim.x * gridDim.y;
-  int lin = blockIdx.x + gridDim.x * blockIdx.y;
-  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-  const int nx = lin % gx, slot = lin / gx;
+  int nx, slot;
+  tile_of<MODE == MODE_FC1 || MODE == MODE_FC2>(gx, nx, slot);
 
   int expert = 0, row0 = slot * BT, limit;
   if (MODE == MODE_PT || MODE == MODE_DENSE_BF16) {
@@ -323,6 +462,9 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
     limit = A.cta_limit[slot];
   }
   const int valid = limit - row0;  // 1..128
+  // in a decode-like batch, slots of at most SKINNY_ROWS rows belong to the skinny kernels of the same op
+  if ((MODE == MODE_FC1 || MODE == MODE_FC2) && valid <= SKINNY_ROWS && skinny_batch(A.cta_limit, A.num_non_exiting[0]))
+    return;
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int m = A.m;
 
@@ -541,102 +683,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   // the ring's last requests (clamped re-reads) must land before the workgroup's LDS is released
   WAIT_VMCNT(0);
 
-  // ---- epilogue: lane (c, g) of tile (ts, rs) holds weight rows 16*rs + 4*g + i, token row c
-  const int wrow0 = nx * BN + wn * 64;  // first weight row of this wave
-  if (MODE == MODE_FC2 || MODE == MODE_DENSE_BF16) {
-    uint16_t* C = reinterpret_cast<uint16_t*>(A.c);
-#pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      const int t = wt * 64 + ts * 16 + c;
-      if (t < valid) {
-        const int64_t p = row0 + t;
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) {
-          const int n = wrow0 + rs * 16 + g * 4;
-          const v4f v = acc[ts][rs];
-          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
-          uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-          uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-          *reinterpret_cast<uint2*>(C + p * m + n) = make_uint2(lo, hi);
-        }
-      }
-    }
-  } else if (MODE == MODE_PT) {
-    uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
-    const float ds = A.d_scale[0];
-#pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      const int t = wt * 64 + ts * 16 + c;
-      if (t < valid) {
-        const int64_t p = row0 + t;
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) {
-          const int n = wrow0 + rs * 16 + g * 4;
-          const v4f v = acc[ts][rs];
-          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
-          const uint32_t o = e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
-          *reinterpret_cast<uint32_t*>(C + p * m + n) = o;
-        }
-      }
-    }
-  } else {  // MODE_FC1: gated SiTU-GLU, e4m3 + ue8m0 block-32 (R128c4) output
-    uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
-    const int half = m >> 1;
-    const float al = A.alpha[expert], be = A.beta[expert];
-    // the wave's 64 interleaved gate/up rows give 32 output columns: one MXFP8 block
-    const int ncol0 = (nx * BN + wn * 64) >> 1;
-    const int blk = ncol0 >> 5;
-#pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      const int t = wt * 64 + ts * 16 + c;
-      // h for 4 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
-      float h[4][2];
-#pragma unroll
-      for (int rs = 0; rs < 4; ++rs) {
-        const v4f v = acc[ts][rs];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const float gg = v[i], uu = v[i + 2];
-          const float sg = 1.0f / (1.0f + __expf(-gg));
-          h[rs][i] = al * tanhf(gg / al) * sg * be * tanhf(uu / be);
-        }
-      }
-      const bool ok = t < valid;
-      const int64_t p = row0 + t;
-      if (ok && A.dbg) {
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs)
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const int n = ncol0 + 8 * rs + 2 * g + i;
-            A.dbg[(p * 3 + 0) * half + n] = acc[ts][rs][i];
-            A.dbg[(p * 3 + 1) * half + n] = acc[ts][rs][i + 2];
-            A.dbg[(p * 3 + 2) * half + n] = h[rs][i];
-          }
-      }
-      uint32_t amax = 0;
-#pragma unroll
-      for (int rs = 0; rs < 4; ++rs)
-#pragma unroll
-        for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[rs][i]) & 0x7fffffffu);
-      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
-      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
-      const uint32_t sc = mx_scale_code(amax);
-      if (ok) {
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) {
-          const int n = ncol0 + 8 * rs + 2 * g;
-          const uint32_t o = mx_code2(h[rs][0], h[rs][1], sc);
-          *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
-        }
-        if (g == 0) {
-          const int64_t kb4 = ((half >> 5) + 3) >> 2;
-          const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
-          A.sf_c[off] = (uint8_t)sc;
-        }
-      }
-    }
-  }
+  bmm_epilogue<MODE>(A, acc, wt, wn, nx, row0, valid, expert, lane);
 }
 
 // the LDS ring of one GEMM workgroup: 4 x (16 + 16) KiB tile stages + 2 x (4 + 2) KiB scale slots = 140 KiB
@@ -645,6 +692,103 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   __shared__ __attribute__((aligned(1024))) uint8_t x0_[LDS_X], x1_[LDS_X], x2_[LDS_X], x3_[LDS_X];          \
   __shared__ __attribute__((aligned(1024))) uint8_t sw0_[LDS_SW], sw1_[LDS_SW], sx0_[LDS_SX], sx1_[LDS_SX]; \
   const BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}}
+
+// Skinny MoE slots (at most SKINNY_ROWS routed rows, e.g. an expert's share of a decode batch): nothing to
+// share through LDS, so no ring and no barrier. A workgroup of 4 waves takes the same 256-row weight tile
+// as the ring kernels; each wave streams its own four weight fragments (rows 64*wave .. +64) and the slot's
+// 16-row activation subtile straight into registers, three k-tiles ahead, and multiplies each k-tile as it
+// lands. Without the ring's LDS several workgroups share a CU, so one's start and end overlap another's
+// streaming. It takes the small slots of decode-sized batches only (skinny_batch); the others exit here
+// and run on the ring kernels.
+template <int MODE>
+KERN_DEV void bmm_skinny(const BmmArgs& A) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gx = A.m / BN;
+  int nx, slot;
+  tile_of<true>(gx, nx, slot);
+  if (slot >= A.num_non_exiting[0]) return;
+  const int expert = A.cta_batch[slot], row0 = slot * BT;
+  const int valid = A.cta_limit[slot] - row0;
+  if (valid > SKINNY_ROWS || !skinny_batch(A.cta_limit, A.num_non_exiting[0])) return;
+  const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
+  const int c = lane & 15, g = lane >> 4;
+  const int rg0 = (nx * BN) >> 4;
+  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)(rg0 + 4 * wave) * KT) * 1024 + lane * 16;
+  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)(rg0 + 4 * wave) * KG) * 256 + lane * 4;
+  // this lane's activation row: rows past the slot read the slot's first row and are never stored
+  const int t = c < valid ? c : 0;
+  const int64_t xrow = MODE == MODE_FC1 ? (int64_t)A.route_map[row0 + t] : (int64_t)(row0 + t);
+  const uint8_t* xp = A.b + xrow * K + 16 * g;
+  const uint8_t* sxp;
+  int sx_kstep;
+  if (A.sf_b_r128c4) {
+    sxp = A.sf_b + 512 * ((xrow >> 7) * (int64_t)(K >> 7)) + (xrow & 31) * 16 + ((xrow & 127) >> 5) * 4 + g;
+    sx_kstep = 512;
+  } else {
+    sxp = A.sf_b + xrow * (K >> 5) + g;
+    sx_kstep = 4;
+  }
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  // register stages: k-tile kt lives in stage kt % 4; the weight-scale dwords of k group kt / 4 in
+  // slot (kt / 4) % 2, read by the MFMA's byte select (kt % 4)
+  v4i wq[4][4], xq[4][2];
+  uint32_t sxq[4], swq[2][4];
+  // k-tile kt, S = kt % 8 (clamped: the prefetches past the end re-read the last tile, never multiplied)
+  auto load = [&](int kt, auto Sc) {
+    constexpr int S = decltype(Sc)::value, st = S & 3, sg = S >> 2;
+    kt = min(kt, KT - 1);
+    if (st == 0) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        swq[sg][f] = *reinterpret_cast<const uint32_t*>(sbase + ((int64_t)f * KG + (kt >> 2)) * 256);
+    }
+#pragma unroll
+    for (int f = 0; f < 4; ++f)  // weights are read once: non-temporal
+      wq[st][f] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wbase + ((int64_t)f * KT + kt) * 1024));
+    // the B operand's two 16-byte chunks of the k-tile, g and g + 4 (the layout the MFMA reads)
+    xq[st][0] = *reinterpret_cast<const v4i*>(xp + (int64_t)kt * 128);
+    xq[st][1] = *reinterpret_cast<const v4i*>(xp + (int64_t)kt * 128 + 64);
+    sxq[st] = sxp[(int64_t)kt * sx_kstep];
+  };
+  auto compute = [&](auto Sc) {
+    constexpr int S = decltype(Sc)::value, st = S & 3, sg = S >> 2;
+    const v8i xb = {xq[st][0][0], xq[st][0][1], xq[st][0][2], xq[st][0][3],
+                    xq[st][1][0], xq[st][1][1], xq[st][1][2], xq[st][1][3]};
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const v8i wb = {wq[st][f][0], wq[st][f][1], wq[st][f][2], wq[st][f][3], 0, 0, 0, 0};
+      acc[0][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb, acc[0][f], 4, 0, st, (int)swq[sg][f], 0,
+                                                                    (int)sxq[st]);
+    }
+  };
+  // the scheduler barriers keep every stage's loads where they are written: sunk towards their use, they
+  // would make each multiply wait for nearly all loads in flight
+#define SKB __builtin_amdgcn_sched_barrier(0)
+  load(0, IC<0>{}); SKB;
+  load(1, IC<1>{}); SKB;
+  load(2, IC<2>{}); SKB;
+  int k0 = 0;
+  for (; k0 + 8 <= KT; k0 += 8) {
+    load(k0 + 3, IC<3>{}); SKB; compute(IC<0>{}); SKB;
+    load(k0 + 4, IC<4>{}); SKB; compute(IC<1>{}); SKB;
+    load(k0 + 5, IC<5>{}); SKB; compute(IC<2>{}); SKB;
+    load(k0 + 6, IC<6>{}); SKB; compute(IC<3>{}); SKB;
+    load(k0 + 7, IC<7>{}); SKB; compute(IC<4>{}); SKB;
+    load(k0 + 8, IC<0>{}); SKB; compute(IC<5>{}); SKB;
+    load(k0 + 9, IC<1>{}); SKB; compute(IC<6>{}); SKB;
+    load(k0 + 10, IC<2>{}); SKB; compute(IC<7>{}); SKB;
+  }
+  if (k0 < KT) {  // K % 1024 == 512: one k group left, tiles k0 .. k0+2 already requested
+    load(k0 + 3, IC<3>{}); SKB;
+    compute(IC<0>{}); SKB; compute(IC<1>{}); SKB; compute(IC<2>{}); SKB; compute(IC<3>{}); SKB;
+  }
+#undef SKB
+  bmm_epilogue<MODE>(A, acc, 0, wave, nx, row0, valid, expert, lane);
+}
 
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
 // a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
@@ -678,6 +822,33 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
   A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
   (void)total_padded;
   bmm_tile<MODE_FC1>(A, L);
+}
+
+// The skinny halves of moe_fc2 / moe_fc1: the same arguments and grid as kern_mx_bmm_fc2 / kern_mx_bmm_fc1,
+// block 256; each takes the slots the other leaves (at most SKINNY_ROWS rows here, more there).
+extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2_skinny(
+    const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
+    const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
+    int sf_b_r128c4, float* dbg) {
+  BmmArgs A = {};
+  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
+  A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
+  A.m = m; A.k = k; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
+  (void)total_padded;
+  bmm_skinny<MODE_FC2>(A);
+}
+
+extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc1_skinny(
+    const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
+    const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
+    const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, float* dbg) {
+  BmmArgs A = {};
+  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.sf_c = sf_c; A.route_map = route_map;
+  A.alpha = alpha; A.beta = beta;
+  A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
+  A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  (void)total_padded;
+  bmm_skinny<MODE_FC1>(A);
 }
 
 // Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).

@@ -18,6 +18,13 @@ from __future__ import annotations
 
 MODULE = "kern_mx"
 BMM_THREADS = 512  # threads of one GEMM workgroup (8 waves)
+SKINNY_THREADS = 256  # threads of one skinny MoE workgroup (4 waves)
+
+
+def _fc_kernels(entry: str) -> list:
+    # an FC op is two launches over the same slot grid and disjoint slot sets: in decode-sized batches the
+    # skinny kernel takes the slots of at most 16 routed rows, the LDS-ring kernel every other slot
+    return [(entry, BMM_THREADS), (entry + "_skinny", SKINNY_THREADS)]
 
 
 def _ceil(a: int, b: int) -> int:
@@ -89,9 +96,15 @@ def moe_routing(topk: int, local_start: int, local_experts: int) -> dict:
     }
 
 
-def _slots(topk: int, experts: int) -> dict:
-    # grid.y: the reference's CTA-slot bound E + ceil(tokens*topk/128) (tools/kernels/abi/trtllm_bmm.py:58-60)
+def slot_bound(topk: int, experts: int) -> dict:
+    """The reference's CTA-slot bound E + ceil(tokens*topk/128) (tools/kernels/abi/trtllm_bmm.py:58-60)."""
     return {"add": [{"ceil_div": [{"mul": ["tokens", topk]}, 128]}, experts]}
+
+
+def _slots(topk: int, experts: int) -> dict:
+    # grid.y: the slot bound rounded up to a multiple of 8, so that the kernels deal the live slots out to
+    # the 8 XCDs in turn (the slots past num_non_exiting exit at once)
+    return {"mul": [{"ceil_div": [slot_bound(topk, experts), 8]}, 8]}
 
 
 def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
@@ -103,12 +116,12 @@ def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
     return {
         "params": p,
         "impl": {"launches": [{
-            "module": MODULE, "entry": "kern_mx_bmm_fc1",
+            "module": MODULE, "entry": entry,
             "params": p + ["i32", "i32", "i64"],
-            "block": [BMM_THREADS, 1, 1],
+            "block": [threads, 1, 1],
             "grid": [m // 256, _slots(topk, experts), 1],
             "args": [{"param": i} for i in range(13)] + [{"i32": m}, {"i32": k}, {"i64": 0}],
-        }]},
+        } for entry, threads in _fc_kernels("kern_mx_bmm_fc1")]},
     }
 
 
@@ -120,12 +133,12 @@ def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
     return {
         "params": p,
         "impl": {"launches": [{
-            "module": MODULE, "entry": "kern_mx_bmm_fc2",
+            "module": MODULE, "entry": entry,
             "params": p + ["i32", "i32", "i32", "i64"],
-            "block": [BMM_THREADS, 1, 1],
+            "block": [threads, 1, 1],
             "grid": [m // 256, _slots(topk, experts), 1],
             "args": [{"param": i} for i in range(9)] + [{"i32": m}, {"i32": k}, {"i32": 1}, {"i64": 0}],
-        }]},
+        } for entry, threads in _fc_kernels("kern_mx_bmm_fc2")]},
     }
 
 
