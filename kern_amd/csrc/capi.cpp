@@ -406,8 +406,8 @@ extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put((void*)c), a.put(num_non_exiting), a.put(total_padded);
   a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(sf_b_r128c4 ? 1 : 0), a.put(dbg);
-  // two launches over disjoint slot sets: in decode-sized batches the slots of at most 16 rows run on the
-  // skinny kernel, every other slot on the LDS-ring kernel
+  // two launches over disjoint slot sets: in decode-sized batches the small slots (at most 32 rows for
+  // FC1, 16 for FC2) run on the skinny kernel, every other slot on the LDS-ring kernel
   int rc = launch("kern_mx_bmm_fc2", (uint32_t)(m / 256), slot_grid(ctas), 1, kBmmThreads, stream, a);
   if (rc != KERN_OK) return rc;
   return launch("kern_mx_bmm_fc2_skinny", (uint32_t)(m / 256), slot_grid(ctas), 1, kSkinnyThreads, stream, a);

@@ -253,8 +253,11 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 //      applied on the global side, each lane fetching the chunk that belongs at its LDS position;
 //   scales once per 512 of K (two slots): W fragments verbatim, X as dwords [k-tile][row].
 enum { MODE_FC2 = 0, MODE_FC1 = 1, MODE_PT = 2, MODE_DENSE_BF16 = 3 };
-// MoE slots with at most this many rows (one 16-row token subtile) run on the skinny kernels
-#define SKINNY_ROWS 16
+// MoE slots with at most this many rows can run on the skinny kernels: two 16-row token subtiles for FC1
+// (K = hidden size: long weight rows), one for FC2 (K = intermediate size: short rows, where the ring
+// kernel's deeper pipeline wins as soon as slots grow)
+template <int MODE>
+constexpr int skinny_rows() { return MODE == MODE_FC1 ? 32 : 16; }
 
 struct BmmArgs {
   const uint8_t* a;      // repacked weights [E][m][k/2]
@@ -427,17 +430,18 @@ KERN_DEV void tile_of(int gx, int& nx, int& slot) {
   slot = lin / gx;
 }
 
-// Whether an MoE launch runs its small slots (at most SKINNY_ROWS rows) on the skinny kernel: when every
+// Whether an MoE launch runs its small slots (at most skinny_rows rows) on the skinny kernel: when every
 // slot of an 8-slot sample spread over the live ones is small, as in decode-sized batches. Otherwise the
 // LDS-ring kernel takes every slot: split, the two launches' tails add up, which costs more than the
 // ring's overhead on the small slots. Every workgroup of both kernels reads the same sample, so the two
 // kernels agree on every slot.
+template <int MODE>
 KERN_DEV bool skinny_batch(const int* cta_limit, int live) {
   bool small = true;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int s = (i * live) >> 3;
-    small = small && cta_limit[s] - s * BT <= SKINNY_ROWS;
+    small = small && cta_limit[s] - s * BT <= skinny_rows<MODE>();
   }
   return small;
 }
@@ -462,8 +466,9 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
     limit = A.cta_limit[slot];
   }
   const int valid = limit - row0;  // 1..128
-  // in a decode-like batch, slots of at most SKINNY_ROWS rows belong to the skinny kernels of the same op
-  if ((MODE == MODE_FC1 || MODE == MODE_FC2) && valid <= SKINNY_ROWS && skinny_batch(A.cta_limit, A.num_non_exiting[0]))
+  // in a decode-like batch, slots of at most skinny_rows rows belong to the skinny kernels of the same op
+  if ((MODE == MODE_FC1 || MODE == MODE_FC2) && valid <= skinny_rows<MODE>() &&
+      skinny_batch<MODE>(A.cta_limit, A.num_non_exiting[0]))
     return;
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int m = A.m;
@@ -693,40 +698,33 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   __shared__ __attribute__((aligned(1024))) uint8_t sw0_[LDS_SW], sw1_[LDS_SW], sx0_[LDS_SX], sx1_[LDS_SX]; \
   const BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}}
 
-// Skinny MoE slots (at most SKINNY_ROWS routed rows, e.g. an expert's share of a decode batch): nothing to
+// Skinny MoE slots (at most skinny_rows routed rows, e.g. an expert's share of a decode batch): nothing to
 // share through LDS, so no ring and no barrier. A workgroup of 4 waves takes the same 256-row weight tile
 // as the ring kernels; each wave streams its own four weight fragments (rows 64*wave .. +64) and the slot's
-// 16-row activation subtile straight into registers, three k-tiles ahead, and multiplies each k-tile as it
-// lands. Without the ring's LDS several workgroups share a CU, so one's start and end overlap another's
-// streaming. It takes the small slots of decode-sized batches only (skinny_batch); the others exit here
-// and run on the ring kernels.
-template <int MODE>
-KERN_DEV void bmm_skinny(const BmmArgs& A) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gx = A.m / BN;
-  int nx, slot;
-  tile_of<true>(gx, nx, slot);
-  if (slot >= A.num_non_exiting[0]) return;
-  const int expert = A.cta_batch[slot], row0 = slot * BT;
-  const int valid = A.cta_limit[slot] - row0;
-  if (valid > SKINNY_ROWS || !skinny_batch(A.cta_limit, A.num_non_exiting[0])) return;
+// one or two 16-row activation subtiles straight into registers, three k-tiles ahead, and multiplies each
+// k-tile as it lands. Without the ring's LDS several workgroups share a CU, so one's start and end overlap
+// another's streaming. It takes the small slots of decode-sized batches only (skinny_batch); the others
+// exit here and run on the ring kernels.
+template <int MODE, int NTS>
+KERN_DEV void skinny_stream(const BmmArgs& A, int nx, int expert, int row0, int valid, int wave, int lane) {
   const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
   const int c = lane & 15, g = lane >> 4;
   const int rg0 = (nx * BN) >> 4;
   const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)(rg0 + 4 * wave) * KT) * 1024 + lane * 16;
   const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)(rg0 + 4 * wave) * KG) * 256 + lane * 4;
-  // this lane's activation row: rows past the slot read the slot's first row and are never stored
-  const int t = c < valid ? c : 0;
-  const int64_t xrow = MODE == MODE_FC1 ? (int64_t)A.route_map[row0 + t] : (int64_t)(row0 + t);
-  const uint8_t* xp = A.b + xrow * K + 16 * g;
-  const uint8_t* sxp;
-  int sx_kstep;
-  if (A.sf_b_r128c4) {
-    sxp = A.sf_b + 512 * ((xrow >> 7) * (int64_t)(K >> 7)) + (xrow & 31) * 16 + ((xrow & 127) >> 5) * 4 + g;
-    sx_kstep = 512;
-  } else {
-    sxp = A.sf_b + xrow * (K >> 5) + g;
-    sx_kstep = 4;
+  // this lane's activation row in each 16-row subtile: rows past the slot read the slot's first row and
+  // are never stored
+  const uint8_t* xp[NTS];
+  const uint8_t* sxp[NTS];
+  const int sx_kstep = A.sf_b_r128c4 ? 512 : 4;
+#pragma unroll
+  for (int ts = 0; ts < NTS; ++ts) {
+    const int t = ts * 16 + c < valid ? ts * 16 + c : 0;
+    const int64_t xrow = MODE == MODE_FC1 ? (int64_t)A.route_map[row0 + t] : (int64_t)(row0 + t);
+    xp[ts] = A.b + xrow * K + 16 * g;
+    sxp[ts] = A.sf_b_r128c4
+                  ? A.sf_b + 512 * ((xrow >> 7) * (int64_t)(K >> 7)) + (xrow & 31) * 16 + ((xrow & 127) >> 5) * 4 + g
+                  : A.sf_b + xrow * (K >> 5) + g;
   }
   v4f acc[4][4];
 #pragma unroll
@@ -735,8 +733,8 @@ KERN_DEV void bmm_skinny(const BmmArgs& A) {
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
   // register stages: k-tile kt lives in stage kt % 4; the weight-scale dwords of k group kt / 4 in
   // slot (kt / 4) % 2, read by the MFMA's byte select (kt % 4)
-  v4i wq[4][4], xq[4][2];
-  uint32_t sxq[4], swq[2][4];
+  v4i wq[4][4], xq[4][NTS][2];
+  uint32_t sxq[4][NTS], swq[2][4];
   // k-tile kt, S = kt % 8 (clamped: the prefetches past the end re-read the last tile, never multiplied)
   auto load = [&](int kt, auto Sc) {
     constexpr int S = decltype(Sc)::value, st = S & 3, sg = S >> 2;
@@ -749,20 +747,26 @@ KERN_DEV void bmm_skinny(const BmmArgs& A) {
 #pragma unroll
     for (int f = 0; f < 4; ++f)  // weights are read once: non-temporal
       wq[st][f] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wbase + ((int64_t)f * KT + kt) * 1024));
-    // the B operand's two 16-byte chunks of the k-tile, g and g + 4 (the layout the MFMA reads)
-    xq[st][0] = *reinterpret_cast<const v4i*>(xp + (int64_t)kt * 128);
-    xq[st][1] = *reinterpret_cast<const v4i*>(xp + (int64_t)kt * 128 + 64);
-    sxq[st] = sxp[(int64_t)kt * sx_kstep];
+#pragma unroll
+    for (int ts = 0; ts < NTS; ++ts) {
+      // the B operand's two 16-byte chunks of the k-tile, g and g + 4 (the layout the MFMA reads)
+      xq[st][ts][0] = *reinterpret_cast<const v4i*>(xp[ts] + (int64_t)kt * 128);
+      xq[st][ts][1] = *reinterpret_cast<const v4i*>(xp[ts] + (int64_t)kt * 128 + 64);
+      sxq[st][ts] = sxp[ts][(int64_t)kt * sx_kstep];
+    }
   };
   auto compute = [&](auto Sc) {
     constexpr int S = decltype(Sc)::value, st = S & 3, sg = S >> 2;
-    const v8i xb = {xq[st][0][0], xq[st][0][1], xq[st][0][2], xq[st][0][3],
-                    xq[st][1][0], xq[st][1][1], xq[st][1][2], xq[st][1][3]};
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const v8i wb = {wq[st][f][0], wq[st][f][1], wq[st][f][2], wq[st][f][3], 0, 0, 0, 0};
-      acc[0][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb, acc[0][f], 4, 0, st, (int)swq[sg][f], 0,
-                                                                    (int)sxq[st]);
+    for (int ts = 0; ts < NTS; ++ts) {
+      const v8i xb = {xq[st][ts][0][0], xq[st][ts][0][1], xq[st][ts][0][2], xq[st][ts][0][3],
+                      xq[st][ts][1][0], xq[st][ts][1][1], xq[st][ts][1][2], xq[st][ts][1][3]};
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const v8i wb = {wq[st][f][0], wq[st][f][1], wq[st][f][2], wq[st][f][3], 0, 0, 0, 0};
+        acc[ts][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb, acc[ts][f], 4, 0, st, (int)swq[sg][f],
+                                                                       0, (int)sxq[st][ts]);
+      }
     }
   };
   // the scheduler barriers keep every stage's loads where they are written: sunk towards their use, they
@@ -788,6 +792,22 @@ KERN_DEV void bmm_skinny(const BmmArgs& A) {
   }
 #undef SKB
   bmm_epilogue<MODE>(A, acc, 0, wave, nx, row0, valid, expert, lane);
+}
+
+template <int MODE>
+KERN_DEV void bmm_skinny(const BmmArgs& A) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gx = A.m / BN;
+  int nx, slot;
+  tile_of<true>(gx, nx, slot);
+  if (slot >= A.num_non_exiting[0]) return;
+  const int expert = A.cta_batch[slot], row0 = slot * BT;
+  const int valid = A.cta_limit[slot] - row0;
+  if (valid > skinny_rows<MODE>() || !skinny_batch<MODE>(A.cta_limit, A.num_non_exiting[0])) return;
+  if (skinny_rows<MODE>() <= 16 || valid <= 16)
+    skinny_stream<MODE, 1>(A, nx, expert, row0, valid, wave, lane);
+  else
+    skinny_stream<MODE, (skinny_rows<MODE>() + 15) / 16>(A, nx, expert, row0, valid, wave, lane);
 }
 
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
@@ -825,7 +845,7 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
 }
 
 // The skinny halves of moe_fc2 / moe_fc1: the same arguments and grid as kern_mx_bmm_fc2 / kern_mx_bmm_fc1,
-// block 256; each takes the slots the other leaves (at most SKINNY_ROWS rows here, more there).
+// block 256; each takes the slots the other leaves (skinny_batch).
 extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2_skinny(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
     const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,

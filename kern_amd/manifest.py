@@ -23,7 +23,8 @@ SKINNY_THREADS = 256  # threads of one skinny MoE workgroup (4 waves)
 
 def _fc_kernels(entry: str) -> list:
     # an FC op is two launches over the same slot grid and disjoint slot sets: in decode-sized batches the
-    # skinny kernel takes the slots of at most 16 routed rows, the LDS-ring kernel every other slot
+    # skinny kernel takes the small slots (at most 32 routed rows for FC1, 16 for FC2), the LDS-ring
+    # kernel every other slot
     return [(entry, BMM_THREADS), (entry + "_skinny", SKINNY_THREADS)]
 
 

@@ -133,7 +133,7 @@ def test_gemm_closed_form_kat(ops):
 
 # --------------------------------------------------------------------------------------- dense e4m3 (config 3 mode)
 
-# M <= 16 takes the skinny path (operands streamed into registers), 17 the LDS ring
+# small M (one live 16-row subtile, or one and a row), ragged M, K not a multiple of 1024
 @pytest.mark.parametrize("M,m,k", [(300, 512, 1024), (4096, 2048, 7168), (5, 512, 1024), (16, 2048, 7168),
                                    (17, 512, 1536)])
 def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
@@ -192,8 +192,8 @@ def _route(ops, oracle, ids, local_start, local):
     return ctas, tabs, dev
 
 
-# decode-sized batches run their slots of at most 16 routed rows on the skinny kernel, the rest on the LDS-ring
-# kernel; mixed and large batches run every slot on the ring kernel (ragged tails)
+# decode-sized batches run their small slots (at most 32 routed rows for FC1, 16 for FC2) on the skinny
+# kernel, the rest on the LDS-ring kernel; mixed and large batches run every slot on the ring kernel
 @pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 4096, 7168), (4, 256, 8, 4096, 7168),
                                        (300, 8, 2, 512, 1024)])
 def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
@@ -201,19 +201,19 @@ def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
 
 
 def _split_ids():
-    """64 tokens, top-2 over 64 experts: each expert takes one or two rows, except expert 5 with 31 (one
-    slot of more than 16 rows that the 8-slot sample 0, 8, .., 56 misses): a decode-like batch whose small
+    """64 tokens, top-2 over 64 experts: each expert takes one or two rows, except expert 5 with 41 (one
+    slot of more than 32 rows that the 8-slot sample 0, 8, .., 56 misses): a decode-like batch whose small
     slots run on the skinny kernel while the ring kernel takes slot 5."""
     ids = np.zeros((64, 2), np.int32)
     for t in range(64):
         ids[t, 0] = t
-        ids[t, 1] = (6 if t == 5 else 5) if t < 31 else (t + 1) % 64
+        ids[t, 1] = (6 if t == 5 else 5) if t < 41 else (t + 1) % 64
     return ids
 
 
 def test_fc_split_batch(ops, oracle):
     ids = _split_ids()
-    print("[fc split] 64 experts, one slot of 31 rows", flush=True)
+    print("[fc split] 64 experts, one slot of 41 rows", flush=True)
     _check_fc1(ops, oracle, ids, 64, 512, 1024)
     _check_fc2(ops, oracle, ids, 64, 512, 1024)
 
