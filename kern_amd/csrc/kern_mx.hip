@@ -1043,86 +1043,107 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_mxfp8(const uint8
 // num_non_exiting[1], total_padded[1], route_map, exp2perm [T*topk]; launch adds i32 T, i32 topk,
 // i32 local_start, i32 E_local (<= 512). One workgroup of 1024 threads; rows of one expert in ascending
 // expanded index, each expert padded to 128-row CTA slots (tables as tools/kernels/abi/trtllm_bmm.py:19-27).
+// A stable counting sort with no serial step: wave w owns the w-th contiguous segment of the expanded
+// indices. (1) Each wave counts its segment per expert (LDS atomics). (2) Per expert, the counts become
+// exclusive prefixes over the waves, the slot counts an exclusive scan over the experts (wave scans), and
+// the slot tables are written. (3) Each wave walks its segment again, 64 indices at a time: the lanes
+// holding expert e OR their lane bits into a per-wave 64-bit mask, so a lane's rank among the lower lanes
+// of its expert is a popcount; the lowest such lane then advances the wave's base for e and clears the
+// mask (one wave's LDS operations execute in program order).
 #define ROUTE_EMAX 512
+KERN_DEV int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
 extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
     const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
     int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
     int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
-  __shared__ int cnt[ROUTE_EMAX];   // per-expert count, then the running rank base
-  __shared__ int off[ROUTE_EMAX];   // per-expert first slot
-  __shared__ int wtab[16][ROUTE_EMAX];  // per-wave count of each expert in the current round
+  __shared__ int wbase[16 * ROUTE_EMAX];                 // [wave][expert]: count, then the wave's next row
+  __shared__ unsigned long long wmask[16 * ROUTE_EMAX];  // [wave][expert]: lanes holding the expert
+  __shared__ int off[ROUTE_EMAX];                        // per-expert first slot
+  __shared__ int wsum[16];
   __shared__ int total_slots;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = T * topk;
-  for (int e = tid; e < E_local; e += 1024) cnt[e] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += 1024) {
+  const int n = T * topk, E = E_local;
+  const int seg = (n + 16 * 64 - 1) / (16 * 64) * 64;  // indices per wave, a multiple of 64
+  const int i_begin = wave * seg, i_end = min(n, i_begin + seg);
+  int* wb = wbase + wave * E;
+  unsigned long long* wm = wmask + wave * E;
+  for (int q = lane; q < E; q += 64) wb[q] = 0, wm[q] = 0ull;
+  // the expert of expanded index i, or -1 when it is not local
+  auto expert_of = [&](int i) -> int {
     const int e = topk_idx[i] - local_start;
-    if (e >= 0 && e < E_local) atomicAdd(&cnt[e], 1);
+    return e >= 0 && e < E ? e : -1;
+  };
+  // (1) per-wave counts (the wave's own table: the clears above came first in program order)
+  for (int i = i_begin + lane; i < i_end; i += 64) {
+    const int e = expert_of(i);
+    if (e >= 0) atomicAdd(&wb[e], 1);
   }
+  __syncthreads();
+  // (2) per expert: exclusive prefix over the waves, total count and slot count
+  int cnt = 0, ns = 0;
+  if (tid < E) {
+    for (int w = 0; w < 16; ++w) {
+      const int c = wbase[w * E + tid];
+      wbase[w * E + tid] = cnt;
+      cnt += c;
+    }
+    ns = (cnt + 127) >> 7;
+  }
+  // exclusive scan of the slot counts over the experts (E <= 512: waves 0..7)
+  const int incl = wave_incl_scan(ns, lane);
+  if (lane == 63) wsum[wave] = incl;
   __syncthreads();
   if (tid == 0) {
     int s = 0;
-    for (int e = 0; e < E_local; ++e) {
-      off[e] = s;
-      s += (cnt[e] + 127) >> 7;
+    for (int w = 0; w < 16; ++w) {
+      const int v = wsum[w];
+      wsum[w] = s;
+      s += v;
     }
     total_slots = s;
     num_non_exiting[0] = s;
     total_padded[0] = s * 128;
   }
   __syncthreads();
-  const int S = total_slots;
-  for (int e = tid; e < E_local; e += 1024) {
-    counts[e] = cnt[e];
-    counts[E_local + e] = off[e];
-    const int ns = (cnt[e] + 127) >> 7;
-    for (int s = 0; s < ns; ++s) {
-      cta_batch[off[e] + s] = e;
-      cta_limit[off[e] + s] = min((off[e] + s + 1) * 128, off[e] * 128 + cnt[e]);
+  if (tid < E) {
+    const int o = wsum[wave] + incl - ns;
+    off[tid] = o;
+    counts[tid] = cnt;
+    counts[E + tid] = o;
+    for (int s2 = 0; s2 < ns; ++s2) {
+      cta_batch[o + s2] = tid;
+      cta_limit[o + s2] = min((o + s2 + 1) * 128, o * 128 + cnt);
     }
   }
+  const int S = total_slots;
   for (int p = tid; p < S * 128; p += 1024) route_map[p] = -1;
-  __syncthreads();
-  for (int e = tid; e < E_local; e += 1024) cnt[e] = 0;
-  for (int base = 0; base < n; base += 1024) {
-    for (int q = tid; q < 16 * ROUTE_EMAX; q += 1024) (&wtab[0][0])[q] = 0;
-    __syncthreads();
-    const int i = base + tid;
-    int e = -1;
-    if (i < n) {
-      e = topk_idx[i] - local_start;
-      if (e < 0 || e >= E_local) e = -1;
-    }
-    // rank among lower lanes of this wave holding the same expert
-    unsigned long long same = 0;
-    unsigned long long pending = __ballot(e >= 0);
-    while (pending) {
-      const int leader = __ffsll((long long)pending) - 1;
-      const int le = __shfl(e, leader);
-      const unsigned long long mk = __ballot(e == le);
-      if (e == le) same = mk;
-      pending &= ~mk;
-    }
-    const int rank = __popcll(same & ((1ull << lane) - 1ull));
-    if (e >= 0 && rank == 0) wtab[wave][e] = __popcll(same);
-    __syncthreads();
+  __syncthreads();  // off[] is complete, and every padding row is written before the rows that fill it
+  // (3) stable ranks, 64 indices of the wave's segment at a time
+  for (int i0 = i_begin; i0 < i_end; i0 += 64) {
+    const int i = i0 + lane;
+    const int e = i < i_end ? expert_of(i) : -1;
+    if (e >= 0) atomicOr(&wm[e], 1ull << lane);
     if (e >= 0) {
-      int before = 0;
-      for (int w2 = 0; w2 < wave; ++w2) before += wtab[w2][e];
-      const int p = off[e] * 128 + cnt[e] + before + rank;
+      const unsigned long long m = wm[e];
+      const int rank = __popcll(m & ((1ull << lane) - 1ull));
+      const int p = off[e] * 128 + wb[e] + rank;
       exp2perm[i] = p;
       route_map[p] = i / topk;
-    } else if (i < n) {
+      if (rank == 0) {  // the expert's lowest lane, after every lane of the group has read the mask
+        wb[e] += __popcll(m);
+        wm[e] = 0ull;
+      }
+    } else if (i < i_end) {
       exp2perm[i] = -1;
     }
-    __syncthreads();
-    for (int e2 = tid; e2 < E_local; e2 += 1024) {
-      int add = 0;
-      for (int w2 = 0; w2 < 16; ++w2) add += wtab[w2][e2];
-      cnt[e2] += add;
-    }
-    __syncthreads();
   }
 }
 

@@ -159,10 +159,16 @@ def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
 
 # --------------------------------------------------------------------------------------- routing
 
-@pytest.mark.parametrize("T,E,k,start,local", [(512, 256, 8, 0, 256), (37, 16, 4, 4, 8), (1, 8, 2, 0, 8),
-                                               (300, 224, 16, 56, 56), (2048, 64, 6, 0, 64)])
-def test_routing_bitexact(ops, oracle, T, E, k, start, local):
+# uniform ids; every token on the same k experts (slots of 128 rows, several per expert); the 512-expert
+# maximum; a segment per wave of several 64-index rounds (T*k = 65536)
+@pytest.mark.parametrize("T,E,k,start,local,skew", [(512, 256, 8, 0, 256, 0), (37, 16, 4, 4, 8, 0),
+                                                    (1, 8, 2, 0, 8, 0), (300, 224, 16, 56, 56, 0),
+                                                    (2048, 64, 6, 0, 64, 0), (1000, 64, 4, 0, 64, 1),
+                                                    (100, 512, 8, 0, 512, 0), (8192, 256, 8, 0, 256, 0)])
+def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
     ids = wl.topk_ids(T * 31 + E, T, E, k)
+    if skew:
+        ids[:] = np.arange(k, dtype=ids.dtype)[None, ::-1] * 3
     ctas = ops.ctas_bound(T, k, local)
     ref = oracle.routing(ids, start, local, ctas_cap=ctas)
     dev = {n: torch.full((s,), -7, dtype=torch.int32, device="cuda") for n, s in
