@@ -303,10 +303,8 @@ struct Args {
 
 // threads of one GEMM workgroup (8 waves)
 constexpr uint32_t kBmmThreads = 512;
-constexpr uint32_t kSkinnyThreads = 256;  // the skinny MoE kernels: 4 waves
-// the slot axis of a MoE GEMM grid: the caller's slot bound rounded up to a multiple of 8, so that the
-// kernels can deal the live slots out to the 8 XCDs in turn (slots past num_non_exiting exit at once)
-static uint32_t slot_grid(int32_t ctas) { return (uint32_t)((ctas + 7) & ~7); }
+// the MoE GEMMs are persistent: one workgroup per CU (MI355X: 256), looping over the live slots' tiles
+constexpr uint32_t kMoeWorkgroups = 256;
 
 int launch(const char* entry, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, void* stream, Args& a,
            uint32_t shared_bytes = 0) {
@@ -406,11 +404,7 @@ extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put((void*)c), a.put(num_non_exiting), a.put(total_padded);
   a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(sf_b_r128c4 ? 1 : 0), a.put(dbg);
-  // two launches over disjoint slot sets: in decode-sized batches the small slots (at most 32 rows for
-  // FC1, 16 for FC2) run on the skinny kernel, every other slot on the LDS-ring kernel
-  int rc = launch("kern_mx_bmm_fc2", (uint32_t)(m / 256), slot_grid(ctas), 1, kBmmThreads, stream, a);
-  if (rc != KERN_OK) return rc;
-  return launch("kern_mx_bmm_fc2_skinny", (uint32_t)(m / 256), slot_grid(ctas), 1, kSkinnyThreads, stream, a);
+  return launch("kern_mx_bmm_fc2", kMoeWorkgroups, 1, 1, kBmmThreads, stream, a);
 }
 
 extern "C" int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a_, const void* sf_a, const void* b,
@@ -429,9 +423,7 @@ extern "C" int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a_, const void* 
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(sf_c), a.put(route_map), a.put(alpha), a.put(beta);
   a.put(num_non_exiting), a.put(total_padded), a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(dbg);
-  int rc = launch("kern_mx_bmm_fc1", (uint32_t)(m / 256), slot_grid(ctas), 1, kBmmThreads, stream, a);
-  if (rc != KERN_OK) return rc;
-  return launch("kern_mx_bmm_fc1_skinny", (uint32_t)(m / 256), slot_grid(ctas), 1, kSkinnyThreads, stream, a);
+  return launch("kern_mx_bmm_fc1", kMoeWorkgroups, 1, 1, kBmmThreads, stream, a);
 }
 
 extern "C" int kern_mxfp4_gemm_e4m3(const void* a_, const void* sf_a, const void* b, const void* sf_b, void* c,

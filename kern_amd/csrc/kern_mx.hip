@@ -253,11 +253,10 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 //      applied on the global side, each lane fetching the chunk that belongs at its LDS position;
 //   scales once per 512 of K (two slots): W fragments verbatim, X as dwords [k-tile][row].
 enum { MODE_FC2 = 0, MODE_FC1 = 1, MODE_PT = 2, MODE_DENSE_BF16 = 3 };
-// MoE slots with at most this many rows can run on the skinny kernels: two 16-row token subtiles for FC1
-// (K = hidden size: long weight rows), one for FC2 (K = intermediate size: short rows, where the ring
-// kernel's deeper pipeline wins as soon as slots grow)
+// MoE slots with at most this many rows take the skinny path (one 16-row token subtile). FC2's weight rows
+// are short (K = intermediate size), and there the ring already wins from 9 rows on.
 template <int MODE>
-constexpr int skinny_rows() { return MODE == MODE_FC1 ? 32 : 16; }
+constexpr int skinny_rows() { return MODE == MODE_FC1 ? 16 : 8; }
 
 struct BmmArgs {
   const uint8_t* a;      // repacked weights [E][m][k/2]
@@ -409,67 +408,34 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
   }
 }
 
-// Workgroup -> (weight tile nx of gx, token slot). The hardware hands workgroups to the 8 XCDs round robin
-// (workgroup lin = x + gridDim.x * y to XCD lin % 8), each XCD with its own L2.
-// MoE grids (slot-major, only a prefix of the slots live, the rest exit at once): slot s runs on XCD s % 8
-// with its gx weight tiles back to back, so the live prefix spreads evenly over all XCDs and a slot's
-// activation tile is shared within one L2; a bijection when gridDim.y % 8 == 0 (the host rounds the slot
-// bound up to that). Dense grids (every tile live): each XCD takes a contiguous run of tiles.
-template <bool MOE>
+// The hardware hands workgroups to the 8 XCDs round robin (workgroup lin = x + gridDim.x * y to XCD
+// lin % 8), each XCD with its own L2.
+// Dense grids (every tile live): workgroup -> (weight tile nx of gx, 128-row block), re-linearized so that
+// each XCD takes a contiguous run of tiles.
 KERN_DEV void tile_of(int gx, int& nx, int& slot) {
   const int total = gridDim.x * gridDim.y;
   int lin = blockIdx.x + gridDim.x * blockIdx.y;
-  if (MOE && (gridDim.y & 7) == 0) {
-    const int j = lin >> 3;
-    nx = j % gx;
-    slot = (j / gx) * 8 + (lin & 7);
-    return;
-  }
-  if (!MOE && (total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
   nx = lin % gx;
   slot = lin / gx;
 }
-
-// Whether an MoE launch runs its small slots (at most skinny_rows rows) on the skinny kernel: when every
-// slot of an 8-slot sample spread over the live ones is small, as in decode-sized batches. Otherwise the
-// LDS-ring kernel takes every slot: split, the two launches' tails add up, which costs more than the
-// ring's overhead on the small slots. Every workgroup of both kernels reads the same sample, so the two
-// kernels agree on every slot.
-template <int MODE>
-KERN_DEV bool skinny_batch(const int* cta_limit, int live) {
-  bool small = true;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int s = (i * live) >> 3;
-    small = small && cta_limit[s] - s * BT <= skinny_rows<MODE>();
-  }
-  return small;
+// MoE tile index lin -> (weight tile nx of gx, slot): slot s belongs to XCD s % 8 (lin % 8), its gx weight
+// tiles back to back, so that the live slots (a prefix) spread evenly over the XCDs and a slot's
+// activation tile is shared within one L2. A bijection on lin >= 0; the slot grows with lin in steps of 8.
+KERN_DEV void moe_tile(int lin, int gx, int& nx, int& slot) {
+  const int j = lin >> 3;
+  nx = j % gx;
+  slot = (j / gx) * 8 + (lin & 7);
 }
 
+// One 128-row (slot or token block) x 256-row (weights) tile on the LDS ring: valid live rows from row0,
+// weights of `expert`.
 template <int MODE>
-KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
+KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int expert, int row0, int valid) {
   // the wave index through readfirstlane: provably uniform, so everything derived from it (the LDS
   // bases of the direct loads) lives in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wt = wave >> 2, wn = wave & 3;  // token half, weight quarter
-  const int gx = A.m / BN;
-  int nx, slot;
-  tile_of<MODE == MODE_FC1 || MODE == MODE_FC2>(gx, nx, slot);
-
-  int expert = 0, row0 = slot * BT, limit;
-  if (MODE == MODE_PT || MODE == MODE_DENSE_BF16) {
-    if (row0 >= A.rows) return;
-    limit = min(A.rows, row0 + BT);
-  } else {
-    if (slot >= A.num_non_exiting[0]) return;
-    expert = A.cta_batch[slot];
-    limit = A.cta_limit[slot];
-  }
-  const int valid = limit - row0;  // 1..128
-  // in a decode-like batch, slots of at most skinny_rows rows belong to the skinny kernels of the same op
-  if ((MODE == MODE_FC1 || MODE == MODE_FC2) && valid <= skinny_rows<MODE>() &&
-      skinny_batch<MODE>(A.cta_limit, A.num_non_exiting[0]))
-    return;
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int m = A.m;
 
@@ -691,27 +657,36 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   bmm_epilogue<MODE>(A, acc, wt, wn, nx, row0, valid, expert, lane);
 }
 
+// Dense modes: one tile per workgroup, grid [m/256, ceil(rows/128)].
+template <int MODE>
+KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
+  int nx, blk;
+  tile_of(A.m / BN, nx, blk);
+  const int row0 = blk * BT;
+  if (row0 >= A.rows) return;
+  bmm_ring_tile<MODE>(A, L, nx, 0, row0, min(A.rows, row0 + BT) - row0);
+}
+
 // the LDS ring of one GEMM workgroup: 4 x (16 + 16) KiB tile stages + 2 x (4 + 2) KiB scale slots = 140 KiB
 #define BMM_LDS_DECL(L)                                                                                  \
   __shared__ __attribute__((aligned(1024))) uint8_t w0_[LDS_W], w1_[LDS_W], w2_[LDS_W], w3_[LDS_W];          \
   __shared__ __attribute__((aligned(1024))) uint8_t x0_[LDS_X], x1_[LDS_X], x2_[LDS_X], x3_[LDS_X];          \
   __shared__ __attribute__((aligned(1024))) uint8_t sw0_[LDS_SW], sw1_[LDS_SW], sx0_[LDS_SX], sx1_[LDS_SX]; \
-  const BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}}
+  BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}}
 
-// Skinny MoE slots (at most skinny_rows routed rows, e.g. an expert's share of a decode batch): nothing to
-// share through LDS, so no ring and no barrier. A workgroup of 4 waves takes the same 256-row weight tile
-// as the ring kernels; each wave streams its own four weight fragments (rows 64*wave .. +64) and the slot's
-// one or two 16-row activation subtiles straight into registers, three k-tiles ahead, and multiplies each
-// k-tile as it lands. Without the ring's LDS several workgroups share a CU, so one's start and end overlap
-// another's streaming. It takes the small slots of decode-sized batches only (skinny_batch); the others
-// exit here and run on the ring kernels.
+// Skinny slots (at most skinny_rows routed rows, e.g. an expert's share of a decode batch): nothing to
+// share through LDS, so no ring and no barrier. Four waves (one half of the workgroup) take a 256-row weight
+// tile of the slot: each wave streams its own four weight fragments (rows 64*w .. +64) over all of K, with
+// the slot's one or two 16-row activation subtiles, straight into registers, three k-tiles ahead,
+// multiplying each k-tile as it lands. The two halves of the workgroup work through their own tiles
+// independently, so one half's start and end overlap the other's streaming.
 template <int MODE, int NTS>
-KERN_DEV void skinny_stream(const BmmArgs& A, int nx, int expert, int row0, int valid, int wave, int lane) {
+KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int valid, int hw, int lane) {
   const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
   const int c = lane & 15, g = lane >> 4;
   const int rg0 = (nx * BN) >> 4;
-  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)(rg0 + 4 * wave) * KT) * 1024 + lane * 16;
-  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)(rg0 + 4 * wave) * KG) * 256 + lane * 4;
+  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)(rg0 + 4 * hw) * KT) * 1024 + lane * 16;
+  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)(rg0 + 4 * hw) * KG) * 256 + lane * 4;
   // this lane's activation row in each 16-row subtile: rows past the slot read the slot's first row and
   // are never stored
   const uint8_t* xp[NTS];
@@ -791,29 +766,70 @@ KERN_DEV void skinny_stream(const BmmArgs& A, int nx, int expert, int row0, int 
     compute(IC<0>{}); SKB; compute(IC<1>{}); SKB; compute(IC<2>{}); SKB; compute(IC<3>{}); SKB;
   }
 #undef SKB
-  bmm_epilogue<MODE>(A, acc, 0, wave, nx, row0, valid, expert, lane);
+  bmm_epilogue<MODE>(A, acc, 0, hw, nx, row0, valid, expert, lane);
 }
 
+// The MoE ops (moe_fc1 / moe_fc2): a persistent grid of one workgroup per CU. Each workgroup owns the
+// 256-row weight tiles lin = blockIdx.x + i * gridDim.x (i = 0, 1, ..; moe_tile with gx = m/256) of the live
+// slots. A pass classifies up to 512 of them at once (one per thread, one cta_limit read each) and
+// compacts the workgroup's tiles into two LDS lists: tiles of slots of more than skinny_rows rows run
+// on the LDS ring with all 8 waves, then the tiles of small slots run on the skinny path, the two halves
+// of the workgroup taking alternate ones without a barrier. The slot grows with i, so the pass whose
+// last candidate lies past the live slots is the last. Both kinds of tile share one launch, so a batch
+// that mixes small and large slots has one tail, and slots past num_non_exiting cost nothing.
 template <int MODE>
-KERN_DEV void bmm_skinny(const BmmArgs& A) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gx = A.m / BN;
-  int nx, slot;
-  tile_of<true>(gx, nx, slot);
-  if (slot >= A.num_non_exiting[0]) return;
-  const int expert = A.cta_batch[slot], row0 = slot * BT;
-  const int valid = A.cta_limit[slot] - row0;
-  if (valid > skinny_rows<MODE>() || !skinny_batch<MODE>(A.cta_limit, A.num_non_exiting[0])) return;
-  if (skinny_rows<MODE>() <= 16 || valid <= 16)
-    skinny_stream<MODE, 1>(A, nx, expert, row0, valid, wave, lane);
-  else
-    skinny_stream<MODE, (skinny_rows<MODE>() + 15) / 16>(A, nx, expert, row0, valid, wave, lane);
+KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nne = A.num_non_exiting[0];
+  const int gx = A.m >> 8, G = gridDim.x;
+  constexpr int kSkinny = skinny_rows<MODE>();
+  for (int base = 0;; base += 512) {
+    int nx, slot;
+    moe_tile(blockIdx.x + G * (base + tid), gx, nx, slot);
+    const int v = slot < nne ? A.cta_limit[slot] - slot * BT : 0;
+    const bool ring = v > kSkinny, skin = v > 0 && v <= kSkinny;
+    __syncthreads();  // the previous pass's tiles are done with the lists and the LDS
+    const unsigned long long br = __ballot(ring), bs = __ballot(skin);
+    if (lane == 0) wcnt[wave] = __popcll(br), wcnt[8 + wave] = __popcll(bs);
+    __syncthreads();
+    int pr = 0, ps = 0, nr = 0, ns = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      pr += w < wave ? wcnt[w] : 0;
+      ps += w < wave ? wcnt[8 + w] : 0;
+      nr += wcnt[w];
+      ns += wcnt[8 + w];
+    }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    if (ring) list[pr + __popcll(br & below)] = base + tid;
+    if (skin) list[512 + ps + __popcll(bs & below)] = base + tid;
+    // the pass's last candidate lies past the live slots: no later pass has work
+    moe_tile(blockIdx.x + G * (base + 511), gx, nx, slot);
+    const bool last = slot >= nne;
+    __syncthreads();
+    for (int e = 0; e < nr; ++e) {
+      moe_tile(blockIdx.x + G * list[e], gx, nx, slot);
+      const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
+      if (e) __syncthreads();  // every wave's LDS reads and landing loads of the previous tile are done
+      bmm_ring_tile<MODE>(A, L, nx, expert, row0, valid);
+    }
+    const int half = wave >> 2, hw = wave & 3;
+    for (int e = half; e < ns; e += 2) {
+      moe_tile(blockIdx.x + G * list[512 + e], gx, nx, slot);
+      const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
+      if (kSkinny <= 16 || valid <= 16)
+        skinny_tile<MODE, 1>(A, nx, expert, row0, valid, hw, lane);
+      else
+        skinny_tile<MODE, (kSkinny + 15) / 16>(A, nx, expert, row0, valid, hw, lane);
+    }
+    if (last) break;
+  }
 }
 
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
 // a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
 // cta_batch, cta_limit; launch adds i32 m, i32 k, i32 sf_b_r128c4, f32* dbg (may be null).
-// Grid [m/256, slots, 1], block 512; slot y >= num_non_exiting[0] exits.
+// Persistent: grid [G, 1, 1] with G a multiple of 8 (one workgroup per CU: 256), block 512 (bmm_moe).
 extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
     const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
@@ -824,12 +840,13 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
   (void)total_padded;
-  bmm_tile<MODE_FC2>(A, L);
+  __shared__ int list[1024], wcnt[16];
+  bmm_moe<MODE_FC2>(A, L, list, wcnt);
 }
 
 // op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
 // c u8 [padded][m/2], sf_c u8 R128c4, route_map, alpha, beta, num_non_exiting, total_padded, cta_batch,
-// cta_limit; launch adds i32 m, i32 k, f32* dbg. Grid [m/256, slots, 1], block 512.
+// cta_limit; launch adds i32 m, i32 k, f32* dbg. Persistent grid [G, 1, 1] as moe_fc2, block 512.
 extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
     const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
@@ -841,34 +858,8 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
   (void)total_padded;
-  bmm_tile<MODE_FC1>(A, L);
-}
-
-// The skinny halves of moe_fc2 / moe_fc1: the same arguments and grid as kern_mx_bmm_fc2 / kern_mx_bmm_fc1,
-// block 256; each takes the slots the other leaves (skinny_batch).
-extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc2_skinny(
-    const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
-    const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
-    int sf_b_r128c4, float* dbg) {
-  BmmArgs A = {};
-  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
-  A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
-  A.m = m; A.k = k; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
-  (void)total_padded;
-  bmm_skinny<MODE_FC2>(A);
-}
-
-extern "C" __global__ __launch_bounds__(256) void kern_mx_bmm_fc1_skinny(
-    const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
-    const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
-    const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, float* dbg) {
-  BmmArgs A = {};
-  A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.sf_c = sf_c; A.route_map = route_map;
-  A.alpha = alpha; A.beta = beta;
-  A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
-  A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
-  (void)total_padded;
-  bmm_skinny<MODE_FC1>(A);
+  __shared__ int list[1024], wcnt[16];
+  bmm_moe<MODE_FC1>(A, L, list, wcnt);
 }
 
 // Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).

@@ -18,14 +18,7 @@ from __future__ import annotations
 
 MODULE = "kern_mx"
 BMM_THREADS = 512  # threads of one GEMM workgroup (8 waves)
-SKINNY_THREADS = 256  # threads of one skinny MoE workgroup (4 waves)
-
-
-def _fc_kernels(entry: str) -> list:
-    # an FC op is two launches over the same slot grid and disjoint slot sets: in decode-sized batches the
-    # skinny kernel takes the small slots (at most 32 routed rows for FC1, 16 for FC2), the LDS-ring
-    # kernel every other slot
-    return [(entry, BMM_THREADS), (entry + "_skinny", SKINNY_THREADS)]
+MOE_WORKGROUPS = 256  # the MoE GEMMs are persistent: one workgroup per CU
 
 
 def _ceil(a: int, b: int) -> int:
@@ -98,48 +91,45 @@ def moe_routing(topk: int, local_start: int, local_experts: int) -> dict:
 
 
 def slot_bound(topk: int, experts: int) -> dict:
-    """The reference's CTA-slot bound E + ceil(tokens*topk/128) (tools/kernels/abi/trtllm_bmm.py:58-60)."""
+    """The reference's CTA-slot bound E + ceil(tokens*topk/128) (tools/kernels/abi/trtllm_bmm.py:58-60): the
+    size of the cta_batch / cta_limit tables."""
     return {"add": [{"ceil_div": [{"mul": ["tokens", topk]}, 128]}, experts]}
-
-
-def _slots(topk: int, experts: int) -> dict:
-    # grid.y: the slot bound rounded up to a multiple of 8, so that the kernels deal the live slots out to
-    # the 8 XCDs in turn (the slots past num_non_exiting exit at once)
-    return {"mul": [{"ceil_div": [slot_bound(topk, experts), 8]}, 8]}
 
 
 def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
     """moe_fc1 = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (13 params); launch adds i32 m (= 2I), i32 k (= H) and a
-    null f32 debug pointer (an i64 zero)."""
+    null f32 debug pointer (an i64 zero). The kernel is persistent: grid [256, 1, 1], and each workgroup
+    loops over the live slots' tiles (num_non_exiting is read on the device), so the grid needs no var."""
     assert m % 256 == 0 and k % 512 == 0
     p = ["in buffer<u8>"] * 4 + ["out buffer<u8>"] * 2 + ["in buffer<i32>", "in buffer<f32>", "in buffer<f32>"] \
         + ["in buffer<i32>"] * 4
     return {
         "params": p,
         "impl": {"launches": [{
-            "module": MODULE, "entry": entry,
+            "module": MODULE, "entry": "kern_mx_bmm_fc1",
             "params": p + ["i32", "i32", "i64"],
-            "block": [threads, 1, 1],
-            "grid": [m // 256, _slots(topk, experts), 1],
+            "block": [BMM_THREADS, 1, 1],
+            "grid": [MOE_WORKGROUPS, 1, 1],
             "args": [{"param": i} for i in range(13)] + [{"i32": m}, {"i32": k}, {"i64": 0}],
-        } for entry, threads in _fc_kernels("kern_mx_bmm_fc1")]},
+        }]},
     }
 
 
 def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
     """moe_fc2 = trtllm_bmm_bf16_mxe2m1_mxe4m3 (9 params); launch adds i32 m (= H), i32 k (= I),
-    i32 sf_b_r128c4 = 1 (FC1 writes its scales R128c4) and a null f32 debug pointer."""
+    i32 sf_b_r128c4 = 1 (FC1 writes its scales R128c4) and a null f32 debug pointer. Persistent grid as
+    moe_fc1."""
     assert m % 256 == 0 and k % 512 == 0
     p = ["in buffer<u8>"] * 4 + ["out buffer<bf16>"] + ["in buffer<i32>"] * 4
     return {
         "params": p,
         "impl": {"launches": [{
-            "module": MODULE, "entry": entry,
+            "module": MODULE, "entry": "kern_mx_bmm_fc2",
             "params": p + ["i32", "i32", "i32", "i64"],
-            "block": [threads, 1, 1],
-            "grid": [m // 256, _slots(topk, experts), 1],
+            "block": [BMM_THREADS, 1, 1],
+            "grid": [MOE_WORKGROUPS, 1, 1],
             "args": [{"param": i} for i in range(9)] + [{"i32": m}, {"i32": k}, {"i32": 1}, {"i64": 0}],
-        } for entry, threads in _fc_kernels("kern_mx_bmm_fc2")]},
+        }]},
     }
 
 

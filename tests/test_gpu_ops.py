@@ -198,8 +198,8 @@ def _route(ops, oracle, ids, local_start, local):
     return ctas, tabs, dev
 
 
-# decode-sized batches run their small slots (at most 32 routed rows for FC1, 16 for FC2) on the skinny
-# kernel, the rest on the LDS-ring kernel; mixed and large batches run every slot on the ring kernel
+# one persistent launch: slots of at most 16 routed rows (FC1; 8 for FC2) take the skinny path, the others
+# the LDS ring; decode-sized batches (all skinny), mixed ones and large ones (ring, ragged tails)
 @pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 4096, 7168), (4, 256, 8, 4096, 7168),
                                        (300, 8, 2, 512, 1024)])
 def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
@@ -207,9 +207,9 @@ def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
 
 
 def _split_ids():
-    """64 tokens, top-2 over 64 experts: each expert takes one or two rows, except expert 5 with 41 (one
-    slot of more than 32 rows that the 8-slot sample 0, 8, .., 56 misses): a decode-like batch whose small
-    slots run on the skinny kernel while the ring kernel takes slot 5."""
+    """64 tokens, top-2 over 64 experts: each expert takes one or two rows, except expert 5 with 41: a
+    decode-like batch whose small slots take the skinny path while slot 5 takes the LDS ring, in the same
+    launch."""
     ids = np.zeros((64, 2), np.int32)
     for t in range(64):
         ids[t, 0] = t

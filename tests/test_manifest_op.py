@@ -69,11 +69,11 @@ def test_k3_grids_match_reference():
     o = mf.moe_ops(3584, 3072, 224, 16)
     # the weight repack: one thread per 16-byte slot, as the reference's fixed grid
     assert o["k3_moe_w_shuffle"]["impl"]["launches"][0]["grid"] == g["k3_moe_w_shuffle"]["grid"]
-    # the CTA-slot axis of both GEMMs is the reference's expression, verbatim, rounded up to a multiple of 8
+    # the reference launches both GEMMs over [m/256, E + ceil(tokens*topk/128)]; ours are persistent (one
+    # workgroup per CU, looping over the live slots on the device), and the slot bound sizes the tables
     for name in ("moe_fc1", "moe_fc2"):
         assert mf.slot_bound(16, 224) == g[name]["grid"][1], name
-        for launch in o[name]["impl"]["launches"]:
-            assert launch["grid"][1] == {"mul": [{"ceil_div": [g[name]["grid"][1], 8]}, 8]}, name
+        assert o[name]["impl"]["launches"][0]["grid"] == [256, 1, 1], name
     # one workgroup per token for the finalize, as the reference launches it
     assert o["moe_finalize_rms"]["impl"]["launches"][0]["grid"] == g["moe_finalize_rms"]["grid"]
 
@@ -84,7 +84,6 @@ def test_plan_grids_and_kernargs(lib, shape, T):
     H, I, E, k = shape["H"], shape["I"], shape["E"], shape["k"]
     o = mf.moe_ops(H, I, E, k)
     v = {"tokens": T}
-    slots = -(-(E + -(-T * k // 128)) // 8) * 8  # the slot bound, rounded up to a multiple of 8
     bufs = lambda n: [0x1000 * (i + 1) for i in range(n)]
 
     p = ops.op_plan(o["moe_quant"], 0, bufs(3) + [T], v)
@@ -96,16 +95,12 @@ def test_plan_grids_and_kernargs(lib, shape, T):
     assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(8)] + [("i", T), ("i", k), ("i", 0), ("i", E)])
 
     p = ops.op_plan(o["moe_fc1"], 0, bufs(13), v)
-    assert p["grid"] == (2 * I // 256, slots, 1) and p["block"] == (512, 1, 1)
+    assert p["grid"] == (256, 1, 1) and p["block"] == (512, 1, 1)
     assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(13)] + [("i", 2 * I), ("i", H), ("q", 0)])
 
     p = ops.op_plan(o["moe_fc2"], 0, bufs(9), v)
-    assert p["grid"] == (H // 256, slots, 1)
+    assert p["grid"] == (256, 1, 1)
     assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(9)] + [("i", H), ("i", I), ("i", 1), ("q", 0)])
-    # the second launch of each FC op: the skinny kernel, same grid and arguments, 4 waves
-    for name, n in (("moe_fc1", 13), ("moe_fc2", 9)):
-        p0, p1 = ops.op_plan(o[name], 0, bufs(n), v), ops.op_plan(o[name], 1, bufs(n), v)
-        assert p1["grid"] == p0["grid"] and p1["args"] == p0["args"] and p1["block"] == (256, 1, 1), name
 
     p = ops.op_plan(o["moe_finalize_rms"], 0, bufs(5) + [T], v)
     assert p["grid"] == (T, 1, 1) and p["block"] == (256, 1, 1)
@@ -210,11 +205,13 @@ def test_dtype_and_direction_checks(lib):
 def test_call_errors(lib):
     o = mf.moe_ops(7168, 2048, 256, 8)
     with pytest.raises(ops.KernError) as e:  # a grid var that is not bound
-        ops.op_plan(o["moe_fc2"], 0, [1] * 9, {})
+        ops.op_plan(o["moe_quant"], 0, [1] * 4, {})
     assert e.value.code == 7 and "unknown var `tokens`" in str(e.value)
     with pytest.raises(ops.KernError) as e:  # wrong number of interface params
         ops.op_plan(o["moe_fc2"], 0, [1] * 8, {"tokens": 1})
     assert e.value.code == 4
+    tall = mf.moe_fc2(7168, 2048, 256, 8)
+    tall["impl"]["launches"][0]["grid"] = [1, mf.slot_bound(8, 256), 1]
     with pytest.raises(ops.KernError) as e:  # grid.y beyond the launch limit
-        ops.op_plan(o["moe_fc2"], 0, [1] * 9, {"tokens": 1 << 20})
+        ops.op_plan(tall, 0, [1] * 9, {"tokens": 1 << 20})
     assert e.value.code == 7 and "exceeds the launch limit" in str(e.value)
