@@ -1179,14 +1179,66 @@ KERN_DEV void moe_combine_chunk(const uint16_t* __restrict__ fc2_out, const int*
                                 const float* __restrict__ topk_w, int t, int H, int topk, int chunk, float acc[8]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int j = 0; j < topk; ++j) {
-    const int row = exp2perm[(int64_t)t * topk + j];
-    const float w = topk_w[(int64_t)t * topk + j];
-    if (row < 0) continue;
-    const v4u xv = *reinterpret_cast<const v4u*>(fc2_out + (int64_t)row * H + chunk * 8);
+  // eight routed rows at a time: all eight loads in flight before the first multiply, then the products
+  // added in routing order (j = 0, 1, ..), skipping rows that are not local
+  for (int j0 = 0; j0 < topk; j0 += 8) {
+    v4u xv[8];
+    float w[8];
+    bool ok[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      acc[e] = __builtin_fmaf(w, bf16_bits_to_f32((xv[e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+    for (int jj = 0; jj < 8; ++jj) {
+      const int j = j0 + jj;
+      const int row = j < topk ? exp2perm[(int64_t)t * topk + j] : -1;
+      w[jj] = j < topk ? topk_w[(int64_t)t * topk + j] : 0.f;
+      ok[jj] = row >= 0;
+      xv[jj] = ok[jj] ? *reinterpret_cast<const v4u*>(fc2_out + (int64_t)row * H + chunk * 8) : (v4u){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (!ok[jj]) continue;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        acc[e] = __builtin_fmaf(w[jj], bf16_bits_to_f32((xv[jj][e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[e]);
+    }
+  }
+}
+
+// moe_combine_chunk for the Q chunks c0 + 256 q of one thread at once (chunks >= nchunks are skipped):
+// the rows of all Q chunks are in flight together; per chunk the sum is the same as moe_combine_chunk's
+template <int Q>
+KERN_DEV void moe_combine_chunks(const uint16_t* __restrict__ fc2_out, const int* __restrict__ exp2perm,
+                                 const float* __restrict__ topk_w, int t, int H, int topk, int c0, int nchunks,
+                                 float acc[Q][8]) {
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[q][e] = 0.f;
+  for (int j0 = 0; j0 < topk; j0 += 8) {
+    v4u xv[Q][8];
+    float w[8];
+    bool ok[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int j = j0 + jj;
+      const int row = j < topk ? exp2perm[(int64_t)t * topk + j] : -1;
+      w[jj] = j < topk ? topk_w[(int64_t)t * topk + j] : 0.f;
+      ok[jj] = row >= 0;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int c = c0 + 256 * q;
+        xv[q][jj] = ok[jj] && c < nchunks ? *reinterpret_cast<const v4u*>(fc2_out + (int64_t)row * H + c * 8)
+                                          : (v4u){0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (!ok[jj]) continue;
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          acc[q][e] = __builtin_fmaf(w[jj], bf16_bits_to_f32((xv[q][jj][e >> 1] >> (16 * (e & 1))) & 0xffffu), acc[q][e]);
+    }
   }
 }
 
@@ -1209,11 +1261,10 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize_rms(
   constexpr int Q = 4;  // chunks per thread kept in registers between the passes (H <= 8192)
   float y[Q][8];
   float ss = 0.f;
+  moe_combine_chunks<Q>(fc2_out, exp2perm, topk_w, t, H, topk, tid, chunks, y);
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
-    const int c = tid + 256 * q;
-    if (c < chunks) {
-      moe_combine_chunk(fc2_out, exp2perm, topk_w, t, H, topk, c, y[q]);
+    if (tid + 256 * q < chunks) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[q][e], y[q][e], ss);
     }
