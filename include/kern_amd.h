@@ -122,6 +122,10 @@ int kern_op_num_launches(kern_op op);
 int kern_op_launch(kern_op op, const uint64_t* params, int nparams, const char* const* var_names,
                    const uint64_t* var_values, int nvars, void* stream);
 
+/* Host-only: parse an op's JSON and run the create-time checks that need no code object (the verifier's,
+ * verify.rs:655-700): KERN_OK or KERN_ERR_MANIFEST with the reason. */
+int kern_op_verify(const char* op_json);
+
 /* Host-only: what kern_op_launch would do for one launch of an op (no device, no code object), for
  * checking a manifest against this ABI without a GPU: grid, block, dynamic LDS bytes and the
  * kernel-argument image (each argument at its natural alignment, bytes<n> aligned to n when n is 1, 2, 4
@@ -132,6 +136,61 @@ int kern_op_plan(const char* op_json, int launch_index, const uint64_t* params, 
                  const char* const* var_names, const uint64_t* var_values, int nvars, uint32_t grid[3],
                  uint32_t block[3], uint32_t* shared_bytes, void* kernargs, size_t cap, size_t* kernargs_size,
                  int* skip);
+
+/* ------------------------------------------------------------------------------------------------
+ * Program runtime (kern_amd/csrc/runtime.cpp): a kern manifest's buffers, modules, ops and programs,
+ * run by program name with var values, as crates/kern-runtime's Runtime (src/lib.rs:137-236) runs them.
+ * One runtime per device, one stream per runtime; every call binds the runtime's device on the calling
+ * thread first (lib.rs:21-23) and calls on one runtime are serialized; graph capture is serialized
+ * process-wide (exec.rs:435-440). The runtime owns every device allocation (compile.rs:289-307).
+ * Served manifest subset: vars, buffers of kind input / output / inout / weight / source / workspace /
+ * carry on the device, modules by file under kernels_dir pinned by sha256, ops whose launches name one
+ * module, programs of one lane with `graph` / `derive`. States, topology, peers, exported or host-placed
+ * buffers, extra lanes and checkpoint binding are KERN_ERR_MANIFEST.
+ * ------------------------------------------------------------------------------------------------ */
+
+typedef struct kern_runtime_s* kern_runtime;
+
+/* Runtime::load (load.rs:44-72): parse and verify the manifest, load each module from kernels_dir (file
+ * = the module's `source`, checked against its `sha256`), create its ops, allocate and zero every buffer
+ * at its vars' maxima, and give input buffers pinned staging. */
+int kern_rt_load(const char* manifest_json, const char* kernels_dir, int gpu, kern_runtime* out);
+int kern_rt_destroy(kern_runtime rt);
+/* The same parse and verification on the host: module files are read and their sha256 checked, ops
+ * verified (kern_op_verify), nothing is created on a device. */
+int kern_rt_check(const char* manifest_json, const char* kernels_dir);
+
+/* Runtime::write_input / read_output (lib.rs:288-330): len bytes from the start of an input / inout
+ * buffer (through its pinned staging) or an output / inout buffer; len <= the buffer's bytes. */
+int kern_rt_write_input(kern_runtime rt, const char* name, const void* data, size_t len);
+int kern_rt_read_output(kern_runtime rt, const char* name, void* data, size_t len);
+/* Harness access to any buffer (harness.rs:30-69). */
+int kern_rt_write_buffer(kern_runtime rt, const char* name, size_t offset, const void* data, size_t len);
+int kern_rt_read_buffer(kern_runtime rt, const char* name, size_t offset, void* data, size_t len);
+/* A weight or source buffer's bytes, whole (what load_weights binds from a checkpoint, load.rs:336). */
+int kern_rt_load_weight(kern_runtime rt, const char* name, const void* data, size_t len);
+/* Run every derive program once, in manifest order, then free the source buffers (derive.rs:72-78).
+ * Required before any other program runs when the manifest has derive programs. */
+int kern_rt_derive(kern_runtime rt);
+
+/* Runtime::run (exec.rs:409-448): issue the program as its manifest says (a `graph` program through its
+ * hipGraph, captured at these var values on first use), then synchronize. var_names / var_values bind
+ * manifest vars (each <= its max). A failed launch is KERN_ERR_CALL with "program `p` call #i (label, op
+ * `o`): op launch #j (entry): ..." (compile.rs:725, exec.rs:707). */
+int kern_rt_run(kern_runtime rt, const char* program, const char* const* var_names, const uint64_t* var_values,
+                int nvars);
+/* Runtime::capture / run_captured (exec.rs:489-548, :636-654): capture the program at these var values
+ * (replacing an earlier graph at the same values); replay a captured graph and synchronize. */
+int kern_rt_capture(kern_runtime rt, const char* program, const char* const* var_names, const uint64_t* var_values,
+                    int nvars);
+int kern_rt_run_captured(kern_runtime rt, const char* program, const char* const* var_names,
+                         const uint64_t* var_values, int nvars);
+/* Runtime::time_captured (harness.rs:252-266): mean milliseconds per replay over iters replays. */
+int kern_rt_time_captured(kern_runtime rt, const char* program, const char* const* var_names,
+                          const uint64_t* var_values, int nvars, int iters, float* ms_per_iter);
+int kern_rt_synchronize(kern_runtime rt);
+/* A buffer's device address and bytes (Runtime::buffer_sizes, lib.rs:243). */
+int kern_rt_buffer(kern_runtime rt, const char* name, void** device_ptr, size_t* bytes);
 
 /* ------------------------------------------------------------------------------------------------
  * Op layer. The library loads its code object kern_mx.hsaco (next to libkern_amd.so unless

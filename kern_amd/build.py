@@ -6,7 +6,8 @@
 2. Its SHA-256 is compiled into libkern_amd.so (the library refuses any other code object) and written
    to kernel_index/kern_mx.toml with the entries and their kernel-argument sizes, the way kern's
    kernel_index pins its modules by digest (tools/kernels/index.py:1-19).
-3. The host side (capi.cpp, manifest_op.cpp; no device code) is compiled with g++ against the HIP runtime.
+3. The host side (capi.cpp, manifest_op.cpp, runtime.cpp; no device code) is compiled with g++ against the HIP
+   runtime.
 """
 from __future__ import annotations
 
@@ -88,7 +89,8 @@ def build_library(sha: str) -> None:
     tmp = LIB + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DKERN_MX_SHA256="{sha}"',
-          os.path.join(CSRC, "capi.cpp"), os.path.join(CSRC, "manifest_op.cpp"), "-o", tmp, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+          os.path.join(CSRC, "capi.cpp"), os.path.join(CSRC, "manifest_op.cpp"), os.path.join(CSRC, "runtime.cpp"),
+          "-o", tmp, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
           "-ldl"])
     os.replace(tmp, LIB)
 

@@ -204,3 +204,87 @@ def moe_ops(H: int, I: int, E: int, topk: int, local_start: int = 0) -> dict:
         "moe_fc2": moe_fc2(H, I, E, topk),
         "moe_finalize_rms": moe_finalize_rms(H, topk),
     }
+
+
+def moe_layer_manifest(H: int, I: int, E: int, topk: int, max_tokens: int, sha256: str,
+                       source: str = "kern_mx.hsaco", eps: float = 1e-6) -> dict:
+    """A whole kern manifest (types.rs:69-97) for one MoE layer of the path on kern_mx, run by the program
+    runtime (kern_rt_*): var `tokens`; raw expert weights as `source` buffers that the `derive_weights`
+    program repacks into `carry` buffers (the K3 derive of head.json:28670); `moe_layer` (launch by launch)
+    and `moe_layer_graph` (hipGraph) = quant -> routing -> FC1 -> FC2 -> finalize_rms, input bf16 `x`,
+    `topk_ids`, `topk_weight`, output bf16 `y`. Table and activation buffers are sized for max_tokens."""
+    slots = E + _ceil(max_tokens * topk, 128)
+    rows = slots * 128
+    T = "tokens"
+
+    def buf(dtype, shape, kind):
+        return {"dtype": dtype, "shape": shape, "kind": kind}
+
+    sf1_bytes = (rows // 128) * 512 * _ceil(I // 32, 4)
+    buffers = {
+        "x": buf("bf16", [T, H], "input"),
+        "topk_ids": buf("i32", [T, topk], "input"),
+        "topk_weight": buf("f32", [T, topk], "input"),
+        "y": buf("bf16", [T, H], "output"),
+        "gamma": buf("bf16", [H], "weight"),
+        "alpha": buf("f32", [E], "weight"),
+        "beta": buf("f32", [E], "weight"),
+        "w13_raw": buf("u8", [E, 2 * I, H // 2], "source"),
+        "s13_raw": buf("u8", [E, 2 * I, H // 32], "source"),
+        "w2_raw": buf("u8", [E, H, I // 2], "source"),
+        "s2_raw": buf("u8", [E, H, I // 32], "source"),
+        "w13": buf("u8", [E, 2 * I, H // 2], "carry"),
+        "s13": buf("u8", [E, 2 * I, H // 32], "carry"),
+        "w2": buf("u8", [E, H, I // 2], "carry"),
+        "s2": buf("u8", [E, H, I // 32], "carry"),
+        "q": buf("u8", [T, H], "workspace"),
+        "qs": buf("u8", [T, H // 32], "workspace"),
+        "counts": buf("i32", [2 * E], "workspace"),
+        "cta_batch": buf("i32", [slots], "workspace"),
+        "cta_limit": buf("i32", [slots], "workspace"),
+        "num_non_exiting": buf("i32", [1], "workspace"),
+        "total_padded": buf("i32", [1], "workspace"),
+        "route_map": buf("i32", [rows], "workspace"),
+        "exp2perm": buf("i32", [T, topk], "workspace"),
+        "c1": buf("u8", [rows, I], "workspace"),
+        "sf1": buf("u8", [sf1_bytes], "workspace"),
+        "c2": buf("bf16", [rows, H], "workspace"),
+    }
+    ops = moe_ops(H, I, E, topk)
+    ops["moe_finalize_rms"] = moe_finalize_rms(H, topk, eps)
+    b = lambda n: {"buf": n}  # noqa: E731
+    i32 = lambda v: {"i32": v}  # noqa: E731
+    tables = [b(n) for n in ("counts", "cta_batch", "cta_limit", "num_non_exiting", "total_padded", "route_map",
+                             "exp2perm")]
+    layer = [
+        {"label": "quant", "op": "moe_quant", "args": [b("x"), b("q"), b("qs"), {"var": T}]},
+        {"label": "routing", "op": "moe_routing", "args": [b("topk_ids")] + tables},
+        {"label": "fc1", "op": "moe_fc1",
+         "args": [b("w13"), b("s13"), b("q"), b("qs"), b("c1"), b("sf1"), b("route_map"), b("alpha"), b("beta"),
+                  b("num_non_exiting"), b("total_padded"), b("cta_batch"), b("cta_limit")]},
+        {"label": "fc2", "op": "moe_fc2",
+         "args": [b("w2"), b("s2"), b("c1"), b("sf1"), b("c2"), b("num_non_exiting"), b("total_padded"),
+                  b("cta_batch"), b("cta_limit")]},
+        {"label": "finalize", "op": "moe_finalize_rms",
+         "args": [b("c2"), b("exp2perm"), b("topk_weight"), b("gamma"), b("y"), {"var": T}]},
+    ]
+    derive = [
+        {"label": "w13", "op": "k3_moe_w_shuffle", "args": [b("w13_raw"), b("w13"), i32(2 * I), i32(H // 2), i32(1)]},
+        {"label": "s13", "op": "k3_moe_sf_shuffle", "args": [b("s13_raw"), b("s13"), i32(2 * I), i32(H // 32), i32(1)]},
+        {"label": "w2", "op": "k3_moe_w_shuffle", "args": [b("w2_raw"), b("w2"), i32(H), i32(I // 2), i32(0)]},
+        {"label": "s2", "op": "k3_moe_sf_shuffle", "args": [b("s2_raw"), b("s2"), i32(H), i32(I // 32), i32(0)]},
+    ]
+    return {
+        "schema_version": 7,
+        "model": f"moe layer H={H} I={I} E={E} top-{topk}",
+        "vars": {T: {"max": max_tokens, "axis": "rows"}},
+        "buffers": buffers,
+        "modules": {MODULE: {"source": source, "sha256": sha256}},
+        "ops": ops,
+        "programs": {
+            "derive_weights": {"derive": True, "calls": derive},
+            "moe_layer": {"calls": layer},
+            "moe_layer_graph": {"graph": True, "calls": layer},
+        },
+    }
+

@@ -84,6 +84,22 @@ _SIGS = {
     "kern_op_launch": [P, P, ctypes.c_int, P, P, ctypes.c_int, P],
     "kern_op_plan": [ctypes.c_char_p, ctypes.c_int, P, ctypes.c_int, P, P, ctypes.c_int, P, P, P, P, ctypes.c_size_t,
                      P, P],
+    "kern_op_verify": [ctypes.c_char_p],
+    "kern_rt_load": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, P],
+    "kern_rt_destroy": [P],
+    "kern_rt_check": [ctypes.c_char_p, ctypes.c_char_p],
+    "kern_rt_write_input": [P, ctypes.c_char_p, P, ctypes.c_size_t],
+    "kern_rt_read_output": [P, ctypes.c_char_p, P, ctypes.c_size_t],
+    "kern_rt_write_buffer": [P, ctypes.c_char_p, ctypes.c_size_t, P, ctypes.c_size_t],
+    "kern_rt_read_buffer": [P, ctypes.c_char_p, ctypes.c_size_t, P, ctypes.c_size_t],
+    "kern_rt_load_weight": [P, ctypes.c_char_p, P, ctypes.c_size_t],
+    "kern_rt_derive": [P],
+    "kern_rt_run": [P, ctypes.c_char_p, P, P, ctypes.c_int],
+    "kern_rt_capture": [P, ctypes.c_char_p, P, P, ctypes.c_int],
+    "kern_rt_run_captured": [P, ctypes.c_char_p, P, P, ctypes.c_int],
+    "kern_rt_time_captured": [P, ctypes.c_char_p, P, P, ctypes.c_int, ctypes.c_int, P],
+    "kern_rt_synchronize": [P],
+    "kern_rt_buffer": [P, ctypes.c_char_p, P, P],
 }
 
 
@@ -450,3 +466,97 @@ class Graph:
             self.close()
         except Exception:
             pass
+
+
+class Runtime:
+    """A kern manifest's buffers, modules, ops and programs on one device (kern_rt_*, the analog of
+    crates/kern-runtime's Runtime, src/lib.rs:137-236): load, write inputs and weights by buffer name,
+    derive, run programs by name with var values, read outputs. Host bytes are numpy arrays or bytes."""
+
+    def __init__(self, manifest: dict | str, kernels_dir: str | None = None, gpu: int = 0):
+        text = manifest if isinstance(manifest, str) else json.dumps(manifest)
+        h = P()
+        check(lib().kern_rt_load(text.encode(), (kernels_dir or os.path.dirname(HSACO_PATH)).encode(), gpu,
+                                 ctypes.byref(h)))
+        self._h = h
+
+    @staticmethod
+    def check(manifest: dict | str, kernels_dir: str | None = None) -> None:
+        """Host-only parse and verification (kern_rt_check): module files read and sha-checked, ops verified."""
+        text = manifest if isinstance(manifest, str) else json.dumps(manifest)
+        check(lib().kern_rt_check(text.encode(), (kernels_dir or os.path.dirname(HSACO_PATH)).encode()))
+
+    def close(self) -> None:
+        if self._h:
+            check(lib().kern_rt_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _bytes(data):
+        import numpy as np
+        a = np.ascontiguousarray(data) if not isinstance(data, (bytes, bytearray)) else np.frombuffer(data, np.uint8)
+        return a, a.ctypes.data, a.nbytes
+
+    def write_input(self, name: str, data) -> None:
+        a, ptr, n = self._bytes(data)
+        check(lib().kern_rt_write_input(self._h, name.encode(), ptr, n))
+
+    def read_output(self, name: str, nbytes: int):
+        import numpy as np
+        out = np.empty(nbytes, np.uint8)
+        check(lib().kern_rt_read_output(self._h, name.encode(), out.ctypes.data, nbytes))
+        return out
+
+    def write_buffer(self, name: str, data, offset: int = 0) -> None:
+        a, ptr, n = self._bytes(data)
+        check(lib().kern_rt_write_buffer(self._h, name.encode(), offset, ptr, n))
+
+    def read_buffer(self, name: str, nbytes: int, offset: int = 0):
+        import numpy as np
+        out = np.empty(nbytes, np.uint8)
+        check(lib().kern_rt_read_buffer(self._h, name.encode(), offset, out.ctypes.data, nbytes))
+        return out
+
+    def load_weight(self, name: str, data) -> None:
+        a, ptr, n = self._bytes(data)
+        check(lib().kern_rt_load_weight(self._h, name.encode(), ptr, n))
+
+    def derive(self) -> None:
+        check(lib().kern_rt_derive(self._h))
+
+    @staticmethod
+    def _vars(vars_: dict | None):
+        names = list((vars_ or {}).keys())
+        arr_n = (ctypes.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+        arr_v = (ctypes.c_uint64 * max(1, len(names)))(*[int(vars_[n]) for n in names])
+        return arr_n, arr_v, len(names)
+
+    def run(self, program: str, vars: dict | None = None) -> None:
+        n, v, k = self._vars(vars)
+        check(lib().kern_rt_run(self._h, program.encode(), n, v, k))
+
+    def capture(self, program: str, vars: dict | None = None) -> None:
+        n, v, k = self._vars(vars)
+        check(lib().kern_rt_capture(self._h, program.encode(), n, v, k))
+
+    def run_captured(self, program: str, vars: dict | None = None) -> None:
+        n, v, k = self._vars(vars)
+        check(lib().kern_rt_run_captured(self._h, program.encode(), n, v, k))
+
+    def time_captured(self, program: str, vars: dict | None = None, iters: int = 10) -> float:
+        n, v, k = self._vars(vars)
+        ms = ctypes.c_float()
+        check(lib().kern_rt_time_captured(self._h, program.encode(), n, v, k, iters, ctypes.byref(ms)))
+        return ms.value
+
+    def buffer(self, name: str) -> tuple[int, int]:
+        ptr, n = P(), ctypes.c_size_t()
+        check(lib().kern_rt_buffer(self._h, name.encode(), ctypes.byref(ptr), ctypes.byref(n)))
+        return ptr.value or 0, n.value
+
