@@ -125,6 +125,36 @@ def timed_loop(torch, stream, fn_step, steps, warmup, graph=True):
     return t0.elapsed_time(t1) / steps, wall / steps
 
 
+def step_samples(torch, stream, fn_step, n=50, warmup=5, distinct=8):
+    """Per-step times beside the back-to-back mean: n steps, each one replay of a one-step HIP graph
+    between two events on `stream` (the first `distinct` step indices are captured, replayed in turn, so
+    a step that rotates inputs keeps rotating). Returns the median and the 10th / 90th percentiles in ms,
+    as the reference's bench reports its samples (docs/bench.md:235-238)."""
+    import numpy as np
+    for i in range(warmup):
+        fn_step(i)
+    torch.cuda.synchronize()
+    graphs = []
+    for i in range(distinct):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn_step(i)
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * n)]
+    with torch.cuda.stream(stream):
+        for i in range(n):
+            ev[2 * i].record(stream)
+            graphs[i % distinct].replay()
+            ev[2 * i + 1].record(stream)
+    torch.cuda.synchronize()
+    t = np.array([ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(n)])
+    return {"n": n, "p10_ms": round(float(np.percentile(t, 10)), 5), "p50_ms": round(float(np.median(t)), 5),
+            "p90_ms": round(float(np.percentile(t, 90)), 5)}
+
+
 def load_traffic(kernel):
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -165,11 +195,12 @@ def bench_gemm(torch, ops, wl, stream, steps, warmup):
     ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
     k_avg, _ = timed_loop(torch, stream, gemm, steps, warmup)
     q_avg, _ = timed_loop(torch, stream, quant, steps, warmup)
+    samples = step_samples(torch, stream, step)
     flop = 2.0 * PM * PN * PK
     q_bytes = PM * PK * 2 + PM * PK + PM * PK // 32
     return {
         "ms_per_step": ms_step, "wall_ms_per_step": wall, "flop": flop, "kernel_ms": k_avg,
-        "quant_ms": q_avg, "quant_bytes": q_bytes, "tensors": (wp, sp, q, qs),
+        "quant_ms": q_avg, "quant_bytes": q_bytes, "tensors": (wp, sp, q, qs), "samples": samples,
     }
 
 
@@ -195,9 +226,10 @@ def bench_decode(torch, ops, wl, stream, steps, warmup, M):
 
     log(f"config 2: timing {steps} launches after {warmup} warm-up")
     ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
+    samples = step_samples(torch, stream, step, distinct=copies)
     nbytes = wbytes + 2 * M * DK + 2 * M * DN
     return {"ms_per_step": ms_step, "kernel_ms": ms_step, "bytes": nbytes,
-            "copies": copies, "x": x, "ws": ws}
+            "copies": copies, "x": x, "ws": ws, "samples": samples}
 
 
 def bench_moe(torch, ops, wl, stream, steps, warmup):
@@ -264,6 +296,7 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
     ms_fc1, _ = timed_loop(torch, stream, lambda i: fc1(), steps, warmup)
     ms_fc2, _ = timed_loop(torch, stream, lambda i: fc2(), steps, warmup)
     ms_fin, _ = timed_loop(torch, stream, lambda i: finalize(), steps, warmup)
+    samples = step_samples(torch, stream, step, distinct=1)
     hit = len(set(ids_np.reshape(-1).tolist()))
     R = MT * MTOP
     b_fc1 = hit * 2 * MI * MH * 17 // 32 + R * MH * 33 // 32 + R * MI * 33 // 32
@@ -272,7 +305,7 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
     b_step = b_fc1 + b_fc2 + b_fin + MT * MH * 2 + MT * MH * 33 // 32 + MT * MTOP * 4
     return {"ms_per_step": ms_step, "wall_ms_per_step": wall, "ms_fc1": ms_fc1, "ms_fc2": ms_fc2, "ms_fin": ms_fin,
             "bytes_fc1": b_fc1, "bytes_fc2": b_fc2, "bytes_fin": b_fin, "bytes_step": b_step, "experts_hit": hit,
-            "slots": ctas}
+            "slots": ctas, "samples": samples}
 
 
 def bench_stack(torch, ops, wl, stream, steps, warmup):
@@ -505,6 +538,7 @@ def main():
                             "kernel": "kern_mx_gemv_bf16", "kernel_us": round(d["kernel_ms"] * 1e3, 3),
 
                             "algorithmic_bytes": d["bytes"]},
+               "samples": d["samples"],
                "config": {"M": args.decode_m, "N": DN, "K": DK, "weight_copies": d["copies"]}}
 
     moe = None
@@ -518,7 +552,7 @@ def main():
         moe = {"metric": "MoE grouped step GB/s (config 4)", "value": round(gbs, 1), "unit": "GB/s",
                "ms_per_step": round(mo["ms_per_step"], 5), "frac": round(gbs / PEAK_HBM_GBS, 4),
                "algorithmic_bytes": mo["bytes_step"],
-               "step": "moe_quant + moe_routing + moe_fc1 + moe_fc2 + moe_finalize_rms",
+               "step": "moe_quant + moe_routing + moe_fc1 + moe_fc2 + moe_finalize_rms", "samples": mo["samples"],
                "fc1": hbm(mo["bytes_fc1"], mo["ms_fc1"], "kern_mx_bmm_fc1"),
                "fc2": hbm(mo["bytes_fc2"], mo["ms_fc2"], "kern_mx_bmm_fc2"),
                "finalize": hbm(mo["bytes_fin"], mo["ms_fin"], "kern_mx_moe_finalize_rms"),
@@ -542,6 +576,7 @@ def main():
 
                          "algorithmic_flop": g["flop"],
                          "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4)},
+            "samples": g["samples"],
             "quantizer": {"kernel": "kern_mx_quant_bf16", "kernel_us": round(g["quant_ms"] * 1e3, 3),
                           "GB/s": round(g["quant_bytes"] / (g["quant_ms"] * 1e-3) / 1e9, 1),
                           "algorithmic_bytes": g["quant_bytes"]},
