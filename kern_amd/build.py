@@ -38,10 +38,10 @@ ENTRIES = {
                           "i32", "i32", "i32"],
     "kern_mx_bmm_fc2": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
                         "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "i32",
-                        "out buffer<f32>"],
+                        "i32", "out buffer<f32>"],
     "kern_mx_bmm_fc1": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<u8>",
                         "out buffer<u8>", "in buffer<i32>", "in buffer<f32>", "in buffer<f32>", "in buffer<i32>",
-                        "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "out buffer<f32>"],
+                        "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "i32", "out buffer<f32>"],
     "kern_mx_gemm_e4m3": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<u8>",
                           "in buffer<f32>", "i32", "i32", "i32", "out buffer<f32>"],
     "kern_mx_gemm_bf16": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",

@@ -403,7 +403,7 @@ extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf
   if (ctas == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put((void*)c), a.put(num_non_exiting), a.put(total_padded);
-  a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(sf_b_r128c4 ? 1 : 0), a.put(dbg);
+  a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(ctas), a.put(sf_b_r128c4 ? 1 : 0), a.put(dbg);
   return launch("kern_mx_bmm_fc2", kMoeWorkgroups, 1, 1, kBmmThreads, stream, a);
 }
 
@@ -422,7 +422,8 @@ extern "C" int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a_, const void* 
   if (ctas == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(sf_c), a.put(route_map), a.put(alpha), a.put(beta);
-  a.put(num_non_exiting), a.put(total_padded), a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(dbg);
+  a.put(num_non_exiting), a.put(total_padded), a.put(cta_batch), a.put(cta_limit), a.put(m), a.put(k), a.put(ctas);
+  a.put(dbg);
   return launch("kern_mx_bmm_fc1", kMoeWorkgroups, 1, 1, kBmmThreads, stream, a);
 }
 

@@ -274,6 +274,7 @@ struct BmmArgs {
   const float* d_scale;  // PT
   float* dbg;            // optional f32 debug output
   int m, k, rows;        // rows: dense M
+  int max_slots;         // MoE: capacity of the slot tables (cta_batch / cta_limit entries)
   int sf_b_r128c4;
 };
 
@@ -780,7 +781,8 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
 template <int MODE>
 KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nne = A.num_non_exiting[0];
+  // the live slots, never more than the tables hold (a corrupt count cannot send reads past them)
+  const int nne = min(A.num_non_exiting[0], A.max_slots);
   const int gx = A.m >> 8, G = gridDim.x;
   constexpr int kSkinny = skinny_rows<MODE>();
   for (int base = 0;; base += 512) {
@@ -828,17 +830,18 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
 
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
 // a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
-// cta_batch, cta_limit; launch adds i32 m, i32 k, i32 sf_b_r128c4, f32* dbg (may be null).
-// Persistent: grid [G, 1, 1] with G a multiple of 8 (one workgroup per CU: 256), block 512 (bmm_moe).
+// cta_batch, cta_limit; launch adds i32 m, i32 k, i32 max_slots (the tables' capacity), i32 sf_b_r128c4,
+// f32* dbg (may be null). Persistent: grid [G, 1, 1] with G a multiple of 8 (one workgroup per CU: 256),
+// block 512 (bmm_moe).
 extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint16_t* c,
     const int* num_non_exiting, const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k,
-    int sf_b_r128c4, float* dbg) {
+    int max_slots, int sf_b_r128c4, float* dbg) {
   BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
-  A.m = m; A.k = k; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
+  A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
   (void)total_padded;
   __shared__ int list[1024], wcnt[16];
   bmm_moe<MODE_FC2>(A, L, list, wcnt);
@@ -846,17 +849,18 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
 
 // op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
 // c u8 [padded][m/2], sf_c u8 R128c4, route_map, alpha, beta, num_non_exiting, total_padded, cta_batch,
-// cta_limit; launch adds i32 m, i32 k, f32* dbg. Persistent grid [G, 1, 1] as moe_fc2, block 512.
+// cta_limit; launch adds i32 m, i32 k, i32 max_slots, f32* dbg. Persistent grid [G, 1, 1] as moe_fc2, block
+// 512.
 extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
     const uint8_t* a, const uint8_t* sf_a, const uint8_t* b, const uint8_t* sf_b, uint8_t* c, uint8_t* sf_c,
     const int* route_map, const float* alpha, const float* beta, const int* num_non_exiting,
-    const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, float* dbg) {
+    const int* total_padded, const int* cta_batch, const int* cta_limit, int m, int k, int max_slots, float* dbg) {
   BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.sf_c = sf_c; A.route_map = route_map;
   A.alpha = alpha; A.beta = beta;
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
-  A.m = m; A.k = k; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = 0; A.dbg = dbg;
   (void)total_padded;
   __shared__ int list[1024], wcnt[16];
   bmm_moe<MODE_FC1>(A, L, list, wcnt);

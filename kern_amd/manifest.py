@@ -96,9 +96,15 @@ def slot_bound(topk: int, experts: int) -> dict:
     return {"add": [{"ceil_div": [{"mul": ["tokens", topk]}, 128]}, experts]}
 
 
+def _slot_capacity(topk: int, experts: int) -> dict:
+    # the capacity of the slot tables, the slot bound at the call's token count, as a 4-byte pack (a launch
+    # arg cannot be an expression)
+    return {"pack": {"size": 4, "fields": [{"at": 0, "expr": slot_bound(topk, experts)}]}}
+
+
 def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
-    """moe_fc1 = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (13 params); launch adds i32 m (= 2I), i32 k (= H) and a
-    null f32 debug pointer (an i64 zero). The kernel is persistent: grid [256, 1, 1], and each workgroup
+    """moe_fc1 = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (13 params); launch adds i32 m (= 2I), i32 k (= H), the slot
+    tables' capacity E + ceil(tokens*topk/128) and a null f32 debug pointer (an i64 zero). The kernel is persistent: grid [256, 1, 1], and each workgroup
     loops over the live slots' tiles (num_non_exiting is read on the device), so the grid needs no var."""
     assert m % 256 == 0 and k % 512 == 0
     p = ["in buffer<u8>"] * 4 + ["out buffer<u8>"] * 2 + ["in buffer<i32>", "in buffer<f32>", "in buffer<f32>"] \
@@ -107,28 +113,30 @@ def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
         "params": p,
         "impl": {"launches": [{
             "module": MODULE, "entry": "kern_mx_bmm_fc1",
-            "params": p + ["i32", "i32", "i64"],
+            "params": p + ["i32", "i32", "bytes<4>", "i64"],
             "block": [BMM_THREADS, 1, 1],
             "grid": [MOE_WORKGROUPS, 1, 1],
-            "args": [{"param": i} for i in range(13)] + [{"i32": m}, {"i32": k}, {"i64": 0}],
+            "args": [{"param": i} for i in range(13)] + [{"i32": m}, {"i32": k}, _slot_capacity(topk, experts),
+                                                         {"i64": 0}],
         }]},
     }
 
 
 def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
-    """moe_fc2 = trtllm_bmm_bf16_mxe2m1_mxe4m3 (9 params); launch adds i32 m (= H), i32 k (= I),
-    i32 sf_b_r128c4 = 1 (FC1 writes its scales R128c4) and a null f32 debug pointer. Persistent grid as
-    moe_fc1."""
+    """moe_fc2 = trtllm_bmm_bf16_mxe2m1_mxe4m3 (9 params); launch adds i32 m (= H), i32 k (= I), the slot
+    tables' capacity, i32 sf_b_r128c4 = 1 (FC1 writes its scales R128c4) and a null f32 debug pointer.
+    Persistent grid as moe_fc1."""
     assert m % 256 == 0 and k % 512 == 0
     p = ["in buffer<u8>"] * 4 + ["out buffer<bf16>"] + ["in buffer<i32>"] * 4
     return {
         "params": p,
         "impl": {"launches": [{
             "module": MODULE, "entry": "kern_mx_bmm_fc2",
-            "params": p + ["i32", "i32", "i32", "i64"],
+            "params": p + ["i32", "i32", "bytes<4>", "i32", "i64"],
             "block": [BMM_THREADS, 1, 1],
             "grid": [MOE_WORKGROUPS, 1, 1],
-            "args": [{"param": i} for i in range(9)] + [{"i32": m}, {"i32": k}, {"i32": 1}, {"i64": 0}],
+            "args": [{"param": i} for i in range(9)] + [{"i32": m}, {"i32": k}, _slot_capacity(topk, experts),
+                                                        {"i32": 1}, {"i64": 0}],
         }]},
     }
 

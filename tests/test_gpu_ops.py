@@ -224,6 +224,34 @@ def test_fc_split_batch(ops, oracle):
     _check_fc2(ops, oracle, ids, 64, 512, 1024)
 
 
+def test_fc2_live_count_is_capped_by_the_tables(ops, oracle):
+    """num_non_exiting larger than the slot tables (a corrupt count): the persistent kernel walks no slot past
+    the tables' capacity; the live slots' rows come out as with the true count (the tables past the routed
+    slots hold -7, which no slot takes as rows)."""
+    T, E, k, m, K = 64, 8, 2, 512, 1024
+    ids = wl.topk_ids(21, T, E, k)
+    ctas, tabs, dev = _route(ops, oracle, ids, 0, E)
+    S = int(tabs["num_non_exiting"][0])
+    for n in ("cta_batch", "cta_limit"):
+        dev[n][S:] = -7
+    rows = ctas * 128
+    q, qs = oracle.quant_mxfp8(wl.activations_bf16(22, rows, K))
+    qs_r = np.zeros(oracle.r128c4_size(rows, K // 32), np.uint8)
+    qs_r[r128c4_offsets(rows, K // 32)] = qs
+    w, sf = wl.mxfp4_weights(23, E, m, K, 118, 126)
+    wp, sfp = ops.repack_weights(to_dev(w), to_dev(sf))
+    outs = []
+    for nne in (S, 1 << 30):
+        dev["num_non_exiting"][0] = nne
+        c = torch.zeros((rows, m), dtype=torch.bfloat16, device="cuda")
+        ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(wp, sfp, to_dev(q), to_dev(qs_r), c, dev["num_non_exiting"],
+                                          dev["total_padded"], dev["cta_batch"], dev["cta_limit"], m=m, k=K,
+                                          ctas=ctas, sf_b_r128c4=True)
+        _sync()
+        outs.append(to_np(c.view(torch.int16)))
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 def _check_fc1(ops, oracle, ids, E, m, K):
     T = ids.shape[0]
     ctas, tabs, dev = _route(ops, oracle, ids, 0, E)

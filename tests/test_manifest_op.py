@@ -96,11 +96,14 @@ def test_plan_grids_and_kernargs(lib, shape, T):
 
     p = ops.op_plan(o["moe_fc1"], 0, bufs(13), v)
     assert p["grid"] == (256, 1, 1) and p["block"] == (512, 1, 1)
-    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(13)] + [("i", 2 * I), ("i", H), ("q", 0)])
+    slots = E + -(-T * k // 128)  # the slot tables' capacity at this token count
+    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(13)] + [("i", 2 * I), ("i", H), ("i", slots),
+                                                                             ("q", 0)])
 
     p = ops.op_plan(o["moe_fc2"], 0, bufs(9), v)
     assert p["grid"] == (256, 1, 1)
-    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(9)] + [("i", H), ("i", I), ("i", 1), ("q", 0)])
+    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(9)] + [("i", H), ("i", I), ("i", slots), ("i", 1),
+                                                                            ("q", 0)])
 
     p = ops.op_plan(o["moe_finalize_rms"], 0, bufs(5) + [T], v)
     assert p["grid"] == (T, 1, 1) and p["block"] == (256, 1, 1)
