@@ -57,11 +57,18 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
 # config 3 (prefill GEMM) and config 2 (decode GEMV) shapes, BASELINE.json configs[2] / configs[1]
 PM, PN, PK = 4096, 2048, 7168
 DN, DK = 18432, 7168
+
+
+def gemv_kernel(M):
+    """The kernel kern_mxfp4_gemv_bf16 launches for config 2 (K = 7168) at M tokens."""
+    return "kern_mx_gemv_bf16_r14" if M <= 2 else "kern_mx_gemv_bf16_p7"
+
 # config 4 (MoE grouped), BASELINE.json configs[3]
 MT, ME, MTOP, MH, MI = 512, 256, 8, 7168, 2048
 # config 5 (layer stack), BASELINE.json configs[4]
 S_LAYERS, S_QKV, S_OIN, S_MS = 4, 9216, 8192, (1, 64, 2048)
 MALL_BYTES = 256 << 20
+WARM_MS = 50.0  # untimed graph replays before each timed one
 
 
 def parse():
@@ -94,7 +101,10 @@ def timed_loop(torch, stream, fn_step, steps, warmup, graph=True):
     """Time `steps` back-to-back steps on `stream`. fn_step(i) enqueues step i. With `graph` the steps
     are captured once into a HIP graph and the graph is replayed, so host-side launch overhead (Python,
     ctypes, a profiler's API hooks) cannot starve the GPU; the timed region is bracketed by
-    synchronize + HIP events on the stream. Returns (ms per step, host wall ms per step)."""
+    synchronize + HIP events on the stream. Before it, after the `warmup` eager steps, the graph is
+    replayed untimed for at least WARM_MS of GPU time: the first replays after an idle period run at
+    lower clocks (a 200-launch decode graph measured 14.4, 14.4, 14.6, 14.0, 13.3, 13.1 us per launch
+    in six consecutive replays). Returns (ms per step, host wall ms per step)."""
     if graph:
         for i in range(warmup):
             fn_step(i)
@@ -103,8 +113,12 @@ def timed_loop(torch, stream, fn_step, steps, warmup, graph=True):
         with torch.cuda.graph(g, stream=stream):
             for i in range(steps):
                 fn_step(i)
-        g.replay()  # untimed replay
-        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        while True:  # untimed replays
+            g.replay()
+            torch.cuda.synchronize()
+            if (time.perf_counter() - w0) * 1e3 >= WARM_MS:
+                break
         run = g.replay
     else:
         for i in range(warmup):
@@ -534,8 +548,8 @@ def main():
                "ms_per_step": round(d["ms_per_step"], 5),
                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                             "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                            "traffic": load_traffic("kern_mx_gemv_bf16"),
-                            "kernel": "kern_mx_gemv_bf16", "kernel_us": round(d["kernel_ms"] * 1e3, 3),
+                            "traffic": load_traffic(gemv_kernel(args.decode_m)),
+                            "kernel": gemv_kernel(args.decode_m), "kernel_us": round(d["kernel_ms"] * 1e3, 3),
 
                             "algorithmic_bytes": d["bytes"]},
                "samples": d["samples"],

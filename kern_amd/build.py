@@ -36,6 +36,12 @@ ENTRIES = {
     "kern_mx_sf_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
     "kern_mx_gemv_bf16": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32", "i32",
                           "i32", "i32", "i32"],
+    "kern_mx_gemv_bf16_rg": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32", "i32",
+                             "i32", "i32"],
+    **{f"kern_mx_gemv_bf16_r{nkt}": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32",
+                                     "i32", "i32"] for nkt in (2, 4, 8, 14, 16)},
+    **{f"kern_mx_gemv_bf16_p{ktw}": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32",
+                                     "i32", "i32", "i32"] for ktw in (1, 2, 4, 7, 8)},
     "kern_mx_bmm_fc2": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
                         "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "in buffer<i32>", "i32", "i32", "i32",
                         "i32", "out buffer<f32>"],

@@ -454,6 +454,37 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
   REQUIRE(M >= 1 && M <= 16 && N > 0 && N % 16 == 0 && K > 0 && K % 512 == 0 && K <= 16384,
           "mxfp4_gemv_bf16: need 1 <= M <= 16, N %% 16 == 0, K %% 512 == 0, K <= 16384 (M=%d N=%d K=%d)", M, N, K);
   REQUIRE(x && w && w_sf && y, "mxfp4_gemv_bf16: null buffer");
+  const int32_t kg = K / 512;
+  // K = 512 * NKT with an unrolled instance for NKT: each of the four waves owns NKT consecutive k-tiles
+  const char* fixed = kg == 2 ? "kern_mx_gemv_bf16_r2" : kg == 4 ? "kern_mx_gemv_bf16_r4" : kg == 8 ? "kern_mx_gemv_bf16_r8"
+                      : kg == 14 ? "kern_mx_gemv_bf16_r14" : kg == 16 ? "kern_mx_gemv_bf16_r16" : nullptr;
+  if (M <= 2 && fixed) {
+    // one workgroup per 16-row group; each wave's x slice (M * NKT * 256 B) in its own LDS region
+    Args a;
+    a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K);
+    return launch(fixed, (uint32_t)(N / 16), 1, 1, 256, stream, a, 2u * (uint32_t)M * (uint32_t)K);
+  }
+  if (M <= 2) {
+    // other K: the same, each wave owning whole 512-wide k groups (a floor or ceiling of KG/4) in a loop,
+    // and keeping their x (1 KiB per token and group) in its own LDS region
+    const int32_t gmax = (kg + 3) / 4;
+    Args a;
+    a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K), a.put(gmax);
+    return launch("kern_mx_gemv_bf16_rg", (uint32_t)(N / 16), 1, 1, 256, stream, a, 4u * (uint32_t)(gmax * M) * 1024u);
+  }
+  static const char* const persistent[9] = {nullptr, "kern_mx_gemv_bf16_p1", "kern_mx_gemv_bf16_p2", nullptr,
+                                            "kern_mx_gemv_bf16_p4", nullptr, nullptr, "kern_mx_gemv_bf16_p7",
+                                            "kern_mx_gemv_bf16_p8"};
+  if (K % 1024 == 0 && K / 1024 <= 8 && persistent[K / 1024]) {
+    // about 256 workgroups of 8 waves, each owning hb <= 9 half groups of 8 rows (at most five 16-row
+    // groups); wave w owns k-tiles [w*K/1024, (w+1)*K/1024) and holds their x in registers
+    const int32_t H = N / 8;
+    const int32_t hb = std::min<int32_t>(9, (H + 255) / 256);
+    Args a;
+    a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K), a.put(hb);
+    return launch(persistent[K / 1024], (uint32_t)((H + hb - 1) / hb), 1, 1, 512, stream, a);
+  }
+  // any other shape: one workgroup per row group, x staged per workgroup in slices
   // sb: k-tiles per wave whose slice of x is staged in LDS at once (at most four 16-byte pieces per lane,
   // M * sb <= 16, sb divides K/512); nb: k-tiles per wave whose weights are in flight together (the
   // largest of the kernel's batch sizes dividing sb)

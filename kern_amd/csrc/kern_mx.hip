@@ -239,6 +239,301 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+// ---------------------------------------------------------------- decode GEMV, M <= 2: one row group per workgroup
+// Same operand mapping as above (fp4 rows decoded by V_CVT_SCALEF32_PK_BF16_FP4 into the A operand of
+// V_MFMA_F32_16X16X32_BF16, tokens in the B columns). One workgroup of four waves per 16-row group, so
+// all N/16 workgroups are resident at once (18 waves per CU at N = 18432). Wave w owns the 512-wide k
+// groups [w*KG/4, (w+1)*KG/4) of its row group, contiguous, so that
+//   * its slice of x (1 KiB per token and k group) goes into a wave-private LDS region with one
+//     buffer->LDS request per KiB, and no workgroup barrier precedes the first multiply;
+//   * one scale dword per k group (the lane's dword of the group's 256 B scale fragment) carries the
+//     scales of all four k-tiles of the group;
+//   * its weight fragments are one contiguous run, streamed four ahead with non-temporal loads.
+// Fewer fragments in flight per wave ran faster than more (4: 12.7 us, 14: 13.6 us at N = 18432,
+// K = 7168); with 18 waves per CU, four in flight already keep HBM saturated.
+// The four partial sums meet in LDS at the end. LDS: 4 * ceil(KG/4) * M KiB (dynamic) + 4 KiB.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16_rg(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,
+    uint16_t* __restrict__ y, int M, int N, int K, int gmax) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xg[];  // [wave][gmax][M][512]
+  __shared__ v4f red[4][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = blockIdx.x;
+  const int KG = K >> 9, KT = K >> 7;
+  const int g0 = (wave * KG) >> 2, ng = (((wave + 1) * KG) >> 2) - g0;
+  const int c = lane & 15, kq = lane >> 4;
+  uint16_t* xw = xg + wave * gmax * M * 512;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, 0x00020000);
+  for (int g = 0; g < ng; ++g)
+    for (int t = 0; t < M; ++t) dma16_buf(xr, (t * K + (g0 + g) * 512) * 2 + lane * 16, xw + (g * M + t) * 512);
+  __builtin_amdgcn_sched_barrier(0);
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wsf + ((int64_t)rg * KG + g0) * 256), (short)0, ng * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + ((int64_t)rg * KT + 4 * g0) * 1024), (short)0, ng * 4096, 0x00020000);
+  // lanes of absent tokens (c >= M) read token 0's x: an MFMA output column depends on its own B column
+  // only, and the columns of absent tokens are never stored
+  // only the lanes of present tokens (c < M) read x: the B columns of absent tokens are never stored, and
+  // an MFMA output column depends on its own B column only, so their registers may hold anything
+  const bool xlive = c < M;
+  const uint16_t* xl = xw + c * 512 + 32 * kq;
+  v4u xb[4] = {};
+  v4f acc[2] = {};
+  if (ng > 0) {
+    uint32_t sc = __builtin_amdgcn_raw_buffer_load_b32(sr, lane * 4, 0, 2);
+    v4u b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      b[u] = __builtin_amdgcn_raw_buffer_load_b128(wr, u * 1024 + lane * 16, 0, 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    WAIT_VMCNT(5);  // requests complete in order: the x slice has landed, the scale and weights may not have
+    // the next group's requests are issued unconditionally (past the last group they point beyond the
+    // buffer and read zeros without touching memory): with a branch around them the compiler's wait
+    // counts would have to assume none were issued and drain every request before each group's last
+    // fragment
+    for (int g = 0; g < ng; ++g) {
+      const int nx = g + 1 < ng ? 0 : 0x40000000;
+      const uint32_t sc_next = __builtin_amdgcn_raw_buffer_load_b32(sr, nx + (g + 1) * 256 + lane * 4, 0, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint16_t* xk = xl + g * M * 512;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float s = e8m0_to_f32((sc >> (8 * u)) & 0xffu);
+        if (xlive) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) xb[jj] = *reinterpret_cast<const v4u*>(xk + u * 128 + jj * 8);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const uint32_t wd = b[u][jj];
+          v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
+          v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
+          v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
+          v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
+          v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, xb[jj]), acc[jj & 1], 0, 0, 0);
+        }
+        b[u] = __builtin_amdgcn_raw_buffer_load_b128(wr, nx + (4 * (g + 1) + u) * 1024 + lane * 16, 0, 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      sc = sc_next;
+    }
+  }
+  red[wave][lane] = acc[0] + acc[1];
+  __syncthreads();
+  if (wave == 0) {
+    const v4f s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    if (c < M) {
+      // lane (c, kq) holds rows 4*kq + i of the group for token c
+      const int n0 = rg * 16 + kq * 4;
+      const uint32_t lo = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
+      const uint32_t hi = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
+      *reinterpret_cast<uint2*>(y + (int64_t)c * N + n0) = make_uint2(lo, hi);
+    }
+  }
+}
+
+// --------------------------------------------- decode GEMV, M <= 2, fixed K: the same, fully unrolled
+// For K = 512 * NKT with NKT in {2, 4, 8, 14, 16} each wave owns exactly NKT consecutive k-tiles (k-tile
+// ranges, not whole 512-wide groups) and its loop is unrolled, so the weight stream has no requests past
+// its end and no branches around them: every request is one the compiler's wait counts can see, and an
+// extra request per wave costs measurably (one unneeded 256 B scale fragment per wave: +0.8 us at N =
+// 18432). The wave's scale fragments (those its k-tiles touch, at most five) go into LDS with one
+// buffer->LDS request beside its x slice; each k-tile reads its scale byte from there.
+template <int NKT>
+KERN_DEV void gemv_rows_fixed(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                              const uint8_t* __restrict__ wsf, uint16_t* __restrict__ y, int M, int N, int K) {
+  constexpr int NSMAX = (NKT + 6) / 4;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xg[];  // [wave][M][NKT * 128]
+  __shared__ v4f red[4][64];
+  __shared__ __attribute__((aligned(16))) uint32_t ssc[4][NSMAX * 64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = blockIdx.x;
+  const int KG = K >> 9, KT = K >> 7;
+  const int kt0 = wave * NKT, kgA = kt0 >> 2;
+  const int ns = ((kt0 + NKT - 1) >> 2) - kgA + 1;  // scale fragments the wave's k-tiles touch
+  const int c = lane & 15, kq = lane >> 4;
+  uint16_t* xw = xg + wave * M * NKT * 128;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, 0x00020000);
+  for (int t = 0; t < M; ++t) {
+#pragma unroll
+    for (int p = 0; p < NKT * 16; p += 64)
+      if (p + lane < NKT * 16) dma16_buf(xr, (t * K + 128 * kt0 + (p + lane) * 8) * 2, xw + t * NKT * 128 + p * 8);
+  }
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wsf + (int64_t)rg * KG * 256), (short)0, KG * 256, 0x00020000);
+  if (lane < ns * 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void_t*)&ssc[wave][0], 16, kgA * 256 + lane * 16, 0, 0, 2);
+  __builtin_amdgcn_sched_barrier(0);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + ((int64_t)rg * KT + kt0) * 1024), (short)0, NKT * 1024, 0x00020000);
+  constexpr int D = NKT < 4 ? NKT : 4;
+  v4u buf[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    buf[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, i * 1024 + lane * 16, 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // requests complete in order: once at most the D weight requests are outstanding, the x slice and the
+  // scale fragments are in LDS (the compiler does not track these buffer->LDS writes into dynamic LDS)
+  WAIT_VMCNT(D);
+  const bool xlive = c < M;
+  const uint16_t* xl = xw + c * NKT * 128 + 32 * kq;
+  const uint8_t* sl = reinterpret_cast<const uint8_t*>(&ssc[wave][0]) + lane * 4;
+  v4u xb[4] = {};
+  v4f acc[2] = {};
+#pragma unroll
+  for (int i = 0; i < NKT; ++i) {
+    const v4u wv = buf[i % D];
+    const int kt = kt0 + i;
+    const float s = e8m0_to_f32(sl[((kt >> 2) - kgA) * 256 + (kt & 3)]);
+    if (xlive) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) xb[jj] = *reinterpret_cast<const v4u*>(xl + i * 128 + jj * 8);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint32_t wd = wv[jj];
+      v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
+      v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
+      v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
+      v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
+      v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, xb[jj]), acc[jj & 1], 0, 0, 0);
+    }
+    if (i + D < NKT) buf[i % D] = __builtin_amdgcn_raw_buffer_load_b128(wr, (i + D) * 1024 + lane * 16, 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  red[wave][lane] = acc[0] + acc[1];
+  __syncthreads();
+  if (wave == 0) {
+    const v4f s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    if (c < M) {
+      const int n0 = rg * 16 + kq * 4;
+      const uint32_t lo = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
+      const uint32_t hi = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
+      *reinterpret_cast<uint2*>(y + (int64_t)c * N + n0) = make_uint2(lo, hi);
+    }
+  }
+}
+
+#define GEMV_ROWS_FIXED(NKT)                                                                                   \
+  extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16_r##NKT(                                   \
+      const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,          \
+      uint16_t* __restrict__ y, int M, int N, int K) {                                                         \
+    gemv_rows_fixed<NKT>(x, w, wsf, y, M, N, K);                                                               \
+  }
+GEMV_ROWS_FIXED(2)
+GEMV_ROWS_FIXED(4)
+GEMV_ROWS_FIXED(8)
+GEMV_ROWS_FIXED(14)
+GEMV_ROWS_FIXED(16)
+#undef GEMV_ROWS_FIXED
+
+// ------------------------------------------------- decode GEMV, 2 < M <= 16: persistent, x held in registers
+// A grid of about 256 workgroups of 8 waves. Workgroup b owns the 8-row half groups [b*hb, (b+1)*hb)
+// (hb = 9 at N = 18432: 72 rows, the same share for every CU), which touch at most five 16-row groups;
+// the half group it shares with a neighbour is loaded with the other half's lanes pointed past the
+// buffer (they read zeros) and only its own rows are stored. Wave w owns k-tiles [w*KTW, (w+1)*KTW)
+// (K = 1024*KTW) of every row group and holds x for them in registers for the whole launch (x is read
+// once per workgroup instead of once per row group: 59 MB of L2 reads at M = 16 against 264 MB), then
+// streams its fragments six ahead. The eight partial sums meet in LDS.
+template <int KTW>
+KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                              const uint8_t* __restrict__ wsf, uint16_t* __restrict__ y, int M, int N, int K, int hb) {
+  constexpr int NG = 5, D = 6, TOT = NG * KTW;
+  __shared__ v4f red[8][NG][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KT = K >> 7, KG = K >> 9;
+  const int H = N >> 3;
+  const int h0 = blockIdx.x * hb, h1 = min(h0 + hb, H);
+  const int g0 = h0 >> 1, ng = ((h1 + 1) >> 1) - g0;  // row groups touched: [g0, g0 + ng), ng <= NG
+  const int c = lane & 15, kq = lane >> 4, r = lane & 15;
+  const int kt0 = wave * KTW, kgA = kt0 >> 2;
+  // x: lane (c, kq) holds x[c][128*kt + 32*kq .. +32] for each of its k-tiles (absent tokens: zeros)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, 0x00020000);
+  const int xoff = c < M ? (c * K + 128 * kt0 + 32 * kq) * 2 : 0x40000000;
+  v4u xv[KTW][4];
+#pragma unroll
+  for (int j = 0; j < KTW; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[j][i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + j * 256 + i * 16, 0, 0);
+  // scale dwords of k groups kgA .. kgA + 2 (KTW <= 8 consecutive k-tiles span at most three groups)
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(wsf + (int64_t)g0 * KG * 256), (short)0, ng * KG * 256, 0x00020000);
+  constexpr int NS = (KTW + 6) / 4;
+  uint32_t sdw[NG][NS];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int kg = kgA + t;
+      sdw[g][t] = __builtin_amdgcn_raw_buffer_load_b32(
+          sr, (g < ng && kg < KG) ? (g * KG + kg) * 256 + lane * 4 : 0x40000000, 0, 2);
+    }
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + (int64_t)g0 * KT * 1024), (short)0, ng * KT * 1024, 0x00020000);
+  // item i = g*KTW + j is fragment (g0 + g, kt0 + j); rows outside the owned half groups read zeros
+  auto woff = [&](int i) -> int {
+    const int g = i / KTW, half = (g0 + g) * 2 + (r >> 3);
+    return (g < ng && half >= h0 && half < h1) ? (g * KT + kt0 + i % KTW) * 1024 + lane * 16 : 0x40000000;
+  };
+  v4u buf[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    if (i < TOT) buf[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff(i), 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  v4f acc[NG][2] = {};
+#pragma unroll
+  for (int i = 0; i < TOT; ++i) {
+    const int g = i / KTW, j = i % KTW, kt = kt0 + j;
+    const v4u wv = buf[i % D];
+    const float s = e8m0_to_f32((sdw[g][(kt >> 2) - kgA] >> (8 * (kt & 3))) & 0xffu);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint32_t wd = wv[jj];
+      v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
+      v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
+      v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
+      v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
+      v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      acc[g][jj & 1] =
+          __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, xv[j][jj]), acc[g][jj & 1], 0, 0, 0);
+    }
+    if (i + D < TOT) buf[i % D] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff(i + D), 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int g = 0; g < NG; ++g) red[wave][g][lane] = acc[g][0] + acc[g][1];
+  __syncthreads();
+  for (int g = wave; g < ng; g += 8) {
+    v4f s = red[0][g][lane];
+#pragma unroll
+    for (int v = 1; v < 8; ++v) s += red[v][g][lane];
+    const int half = (g0 + g) * 2 + (kq >> 1);
+    if (c < M && half >= h0 && half < h1) {
+      const int n0 = (g0 + g) * 16 + kq * 4;
+      const uint32_t lo = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
+      const uint32_t hi = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
+      *reinterpret_cast<uint2*>(y + (int64_t)c * N + n0) = make_uint2(lo, hi);
+    }
+  }
+}
+
+#define GEMV_PERSISTENT(KTW)                                                                                   \
+  extern "C" __global__ __launch_bounds__(512) void kern_mx_gemv_bf16_p##KTW(                                   \
+      const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,          \
+      uint16_t* __restrict__ y, int M, int N, int K, int hb) {                                                 \
+    gemv_persistent<KTW>(x, w, wsf, y, M, N, K, hb);                                                           \
+  }
+GEMV_PERSISTENT(1)
+GEMV_PERSISTENT(2)
+GEMV_PERSISTENT(4)
+GEMV_PERSISTENT(7)
+GEMV_PERSISTENT(8)
+#undef GEMV_PERSISTENT
+
 // ====================================================================================== block-scaled GEMM
 // One workgroup computes a 128-row (token/slot) x 256-row (weight) tile with 8 waves (two per SIMD) in a
 // 2x4 grid; each wave owns 64 x 64 = 4 x 4 tiles of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (A = fp4 weights,

@@ -88,14 +88,28 @@ def test_repack_bitexact(ops, oracle, gated):
 
 # --------------------------------------------------------------------------------------- decode GEMV
 
+# kern_mxfp4_gemv_bf16 picks a kernel by shape; the cases cover each:
+#   M <= 2, K = 512 * {2, 4, 8, 14, 16} -> kern_mx_gemv_bf16_r{2,4,8,14,16} (unrolled);
+#   M <= 2, other K -> kern_mx_gemv_bf16_rg (k groups split four ways: KG = 1, 3, 7, 32);
+#   M > 2, K = 1024 * {1, 2, 4, 7, 8} -> kern_mx_gemv_bf16_p{1,2,4,7,8} (half-group shares of 1 and 9,
+#   a ragged last workgroup at N = 18448);
+#   anything else -> kern_mx_gemv_bf16 (K = 1536, 3072).
 @pytest.mark.parametrize("M,N,K,lo,hi", [(8, 512, 1024, 124, 130), (1, 18432, 7168, 122, 132),
                                          (4, 18432, 7168, 122, 132), (16, 18432, 7168, 122, 132),
-                                         (3, 1024, 2048, 100, 150)])
+                                         (3, 1024, 2048, 100, 150),
+                                         (1, 16, 512, 118, 136), (2, 48, 1536, 122, 132), (2, 32, 3584, 122, 132),
+                                         (2, 9216, 7168, 122, 132), (1, 64, 16384, 122, 132),
+                                         (5, 4096, 4096, 122, 132), (16, 7168, 8192, 122, 132),
+                                         (7, 18448, 7168, 122, 132), (12, 1040, 7168, 122, 132),
+                                         (5, 256, 1536, 122, 132), (16, 512, 3072, 122, 132),
+                                         (1, 512, 1024, 122, 132), (2, 1024, 2048, 122, 132),
+                                         (1, 2048, 4096, 122, 132), (1, 7168, 8192, 122, 132),
+                                         (2, 112, 8192, 118, 136)])
 def test_gemv_w4a16(ops, oracle, M, N, K, lo, hi):
     x = wl.activations_bf16(100 + M, M, K)
     w, sf = wl.mxfp4_weights(200 + M, 1, N, K, lo, hi)
     wp, sfp = ops.repack_weights(to_dev(w[0]), to_dev(sf[0]))
-    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")  # rows never stored stay NaN
     ops.mxfp4_gemv_bf16(to_dev(x), wp, sfp, y, M, N=N, K=K)
     _sync()
     _, yf = oracle.gemv_w4a16(x, w[0], sf[0])
