@@ -558,7 +558,7 @@ extern "C" int kern_mxfp8_gemm_bf16(const void* a, const void* w, void* c, const
   if (k == 0) return fail(KERN_ERR_API, "cublaslt_mxfp8_tn: k == 0 leaves c undefined; zero it instead");
   Args x;
   x.put(a), x.put(w), x.put(c), x.put(a_sf), x.put(w_sf), x.put(m), x.put(n), x.put(k), x.put(ldc);
-  return launch("kern_mx_gemm_mxfp8", (uint32_t)((n + 127) / 128), (uint32_t)((m + 127) / 128), 1, 256, stream, x);
+  return launch("kern_mx_gemm_mxfp8", (uint32_t)((n + 255) / 256), (uint32_t)((m + 127) / 128), 1, 512, stream, x);
 }
 
 // weight_prep family: one thread per element, 256 per workgroup (tools/kernels-src/weight_prep.cu)

@@ -1192,54 +1192,99 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_bf16(const uint8_
 // elements of K in the 128x4 tiled layout (rows padded to 128, k blocks to 4; block (r/128, b/4) at
 // 512 (r/128 * ceil(K/128) + b/4), entry (r, b) at (r%32)*16 + (r%128/32)*4 + b%4). K % 32 == 0.
 //
-// One workgroup of 4 waves computes a 128 (m) x 128 (n) tile, wave (wm, wn) = 64 x 64, on
-// V_MFMA_SCALE_F32_16X16X128_F8F6F4 with W as the A operand and A as the B operand (so each lane ends
-// with four consecutive n of one m). Both operands go from memory straight into LDS (buffer loads: reads
-// past an operand's end return zeros; rows past m or n read the last valid row and are never stored),
-// 16-byte chunk j of row t at t*128 + ((j ^ ((t>>1)&7)) << 4), double-buffered over 128-wide k-tiles.
-// Each k-tile's two 512-byte scale blocks are staged alongside. In the last k-tile, when K % 128 != 0,
-// the chunks past K are zeroed in registers and the scale bytes of k blocks past K read as 1.0.
-#define G8_LDS_T 16384  // one operand tile: 128 rows x 128 B
-#define G8_LDS_STAGE (2 * G8_LDS_T + 1024)
+// One workgroup of 8 waves (two per SIMD) computes a 128 (m) x 256 (n) tile, wave (wm, wn) = 64 x 64 in a
+// 2 x 4 grid, on V_MFMA_SCALE_F32_16X16X128_F8F6F4 with W as the A operand and A as the B operand (so each
+// lane ends with four consecutive n of one m). Both operands go from memory straight into LDS (buffer
+// loads: reads past an operand's end return zeros; rows past m or n read the last valid row and are
+// never stored), 16-byte chunk j of row t at t*128 + ((j ^ ((t>>1)&7)) << 4), through a three-stage ring
+// two k-tiles ahead of the MFMAs with one workgroup barrier per k-tile. Each stage is its own __shared__
+// variable and the loop is unrolled by three, so that the compiler's wait counts for a stage's reads
+// do not include the requests still landing in the other stages (with one runtime-selected buffer pair
+// it waited for every request before each tile's reads, and loads never overlapped the MFMAs).
+// Every wave issues the same seven requests per k-tile: two 1 KiB pieces of the A tile, four of the W
+// tile and 48 dwords of the tile's three 512-byte scale blocks (A's, W's two), so one count fits all.
+// In the last k-tile, when K % 128 != 0, the chunks past K are zeroed in registers and the scale bytes
+// of k blocks past K read as 1.0.
+// Buffer -> LDS requests written as inline asm, for kern_mx_gemm_mxfp8 only: the compiler does not see
+// them as LDS writes, so it adds no wait of its own before the tile's LDS reads (its alias analysis
+// could not tell the stage being read from the stages still filling and waited for every request). The
+// kernel orders them itself: explicit request counts and a barrier per k-tile, and it issues no other
+// vector-memory loads that the compiler would count. M0 carries the wave's LDS base; nothing else in
+// that kernel uses M0 (checked in its code object).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+KERN_DEV void lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, const void* lds_wave_base) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(const lds_void_t*)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+KERN_DEV void lds_dma4(__amdgpu_buffer_rsrc_t r, int voff, const void* lds_wave_base) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(const lds_void_t*)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
-extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_mxfp8(const uint8_t* __restrict__ a,
+#define G8_XT 16384                  // A tile: 128 rows x 128 B
+#define G8_WT 32768                  // W tile: 256 rows x 128 B
+#define G8_STAGE (G8_XT + G8_WT + 2048)  // + scale blocks: A's, then W's two, and 512 B of pad
+
+extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8_t* __restrict__ a,
                                                                      const uint8_t* __restrict__ w,
                                                                      uint16_t* __restrict__ c,
                                                                      const uint8_t* __restrict__ a_sf,
                                                                      const uint8_t* __restrict__ w_sf, int M, int N,
                                                                      int K, int ldc) {
-  __shared__ __attribute__((aligned(1024))) uint8_t st0[G8_LDS_STAGE], st1[G8_LDS_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t st0[G8_STAGE], st1[G8_STAGE], st2[G8_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * 128, n0 = blockIdx.x * 128;
+  const int wm = wave >> 2, wn = wave & 3;
+  // tile: each XCD takes a contiguous run of the (m, n) tiles (as tile_of)
+  const int gxn = gridDim.x, total = gridDim.x * gridDim.y;
+  int lin = blockIdx.x + gxn * blockIdx.y;
+  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  const int m0 = (lin / gxn) * 128, n0 = (lin % gxn) * 256;
   const int KT = (K + 127) >> 7, KB = K >> 5, kb4 = (KB + 3) >> 2;
+  const int mt = (M + 127) >> 7, nt = (N + 127) >> 7;
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)a, (short)0, M * K, 0x00020000);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, N * K, 0x00020000);
-  const int mt = (M + 127) >> 7, nt = (N + 127) >> 7;
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)a_sf, (short)0, mt * kb4 * 512, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)w_sf, (short)0, nt * kb4 * 512, 0x00020000);
-  // this lane's source rows and 16-byte chunk for request r (rows 32r + 8*wave + lane/8)
-  int offa[4], offw[4];
+  // this lane's source row and 16-byte chunk for request r of each operand (rows 64r + 8*wave + lane/8)
+  int offa[2], offw[4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int t = 64 * r + 8 * wave + (lane >> 3);
+    offa[r] = min(m0 + t, M - 1) * K + (((lane & 7) ^ ((t >> 1) & 7)) << 4);
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int t = 32 * r + 8 * wave + (lane >> 3);
-    const int chunk = ((lane & 7) ^ ((t >> 1) & 7)) << 4;
-    offa[r] = min(m0 + t, M - 1) * K + chunk;
-    offw[r] = min(n0 + t, N - 1) * K + chunk;
+    const int t = 64 * r + 8 * wave + (lane >> 3);
+    offw[r] = min(n0 + t, N - 1) * K + (((lane & 7) ^ ((t >> 1) & 7)) << 4);
   }
-  // scale blocks: waves 0-1 bring the two halves of A's block, waves 2-3 W's
-  const __amdgpu_buffer_rsrc_t rs = wave < 2 ? rsa : rsw;
-  const int sbase = (wave < 2 ? blockIdx.y : blockIdx.x) * kb4 * 512 + (wave & 1) * 256 + lane * 4;
+  // scale dword d = 64 * wave + lane: d < 128 from A's 512-byte block of the k-tile, then W's two blocks
+  // (a block past the last 128 rows of W re-reads the last one: its rows are never stored); waves 6 and
+  // 7 re-read A's first dword into the pad, so that every lane of every wave issues the same request
+  // (a wave reads one array: waves 0-1 A's, 2-5 W's, 6-7 A's again, so its buffer resource is uniform)
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)a_sf, (short)0, mt * kb4 * 512, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)w_sf, (short)0, nt * kb4 * 512, 0x00020000);
+  const bool s_w = wave >= 2 && wave < 6;
+  const __amdgpu_buffer_rsrc_t rs = s_w ? rsw : rsa;
+  const int soff = wave < 2 ? ((m0 >> 7) * kb4) * 512 + (64 * wave + lane) * 4
+                   : s_w    ? (min((n0 >> 7) + ((wave - 2) >> 1), nt - 1) * kb4) * 512 + (((wave - 2) & 1) * 64 + lane) * 4
+                            : ((m0 >> 7) * kb4) * 512;
+  // this lane's chunk within each k-tile (the same for all of its requests: 64r + 8*wave keeps t/2 % 8)
+  const int jb = ((lane & 7) ^ (((8 * wave + (lane >> 3)) >> 1) & 7)) << 4;
   auto dma_tile = [&](int kt, uint8_t* stg) {
+    kt = min(kt, KT - 1);  // requests past the last tile re-read it into a stage that is never multiplied
+    // chunks past K (a partial last k-tile) read from past the buffer's end: zeros, so the MFMAs need
+    // no masks. The offsets pass through an empty asm so that no copy of them is kept per step.
+    int oa[2] = {offa[0], offa[1]}, ow[4] = {offw[0], offw[1], offw[2], offw[3]};
+    asm volatile("" : "+v"(oa[0]), "+v"(oa[1]), "+v"(ow[0]), "+v"(ow[1]), "+v"(ow[2]), "+v"(ow[3]));
+    const bool in_k = kt * 128 + jb < K;  // 0xFFFFFFF0 lies past any operand (they are below 2 GiB)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) lds_dma16(ra, in_k ? oa[r] + kt * 128 : (int)0xFFFFFFF0u, stg + (r * 8 + wave) * 1024);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(stg + (r * 4 + wave) * 1024), 16, offa[r] + kt * 128, 0, 0, 0);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(stg + G8_LDS_T + (r * 4 + wave) * 1024), 16,
-                                               offw[r] + kt * 128, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(stg + 2 * G8_LDS_T + (wave >> 1) * 512 + (wave & 1) * 256),
-                                             4, sbase + kt * 512, 0, 0, 0);
+      lds_dma16(rw, in_k ? ow[r] + kt * 128 : (int)0xFFFFFFF0u, stg + G8_XT + (r * 8 + wave) * 1024);
+    lds_dma4(rs, soff + kt * 512, stg + G8_XT + G8_WT + wave * 256);
   };
 
   v4f acc[4][4];
@@ -1247,65 +1292,79 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_mxfp8(const uint8
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-  const int cl = lane & 15, g = lane >> 4;
 
   auto tile = [&](const uint8_t* stg, bool last) {
-    // operands: n subtiles (A operand, from W) and m subtiles (B operand, from A)
-    v8i wo[4], ao[4];
-    uint32_t sw_[4], sa_[4];
-    const int kr = K & 127;  // valid bytes of a partial last tile
-    const bool v0 = !last || kr == 0 || 16 * g < kr, v1 = !last || kr == 0 || 64 + 16 * g < kr;
-    const bool vs = !last || kr == 0 || 32 * g < kr;
+    // operands: n subtiles (A operand, from W), then the m subtiles (B operand, from A) in two halves,
+    // each multiplied as it lands (fewer operand registers live at once)
+    v8i wo[4], ao[2];
+    uint32_t sw_[4], sa_[2];
+    const uint8_t* sc = stg + G8_XT + G8_WT;
+    // the lane coordinates pass through an empty asm, so that the LDS addresses derived from them are
+    // computed here, per tile, instead of being hoisted out of the loop for every copy of the unrolled
+    // steps (which ran out of registers)
+    int cl = lane & 15, g = lane >> 4;
+    asm volatile("" : "+v"(cl), "+v"(g));
+    const int kr = K & 127;  // valid bytes of a partial last tile (its chunks past K are zeros)
+    const bool vs = !last || kr == 0 || 32 * g < kr;  // this lane's k block lies within K
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      {
-        const int t = wn * 64 + q * 16 + cl;
-        const uint8_t* row = stg + G8_LDS_T + t * 128;
-        const int sw = (t >> 1) & 7;
-        v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
-        v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
-        if (!v0) x0 = (v4i){0, 0, 0, 0};
-        if (!v1) x1 = (v4i){0, 0, 0, 0};
-        wo[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        sw_[q] = vs ? stg[2 * G8_LDS_T + 512 + (t & 31) * 16 + (t >> 5) * 4 + g] : 127u;
-      }
-      {
-        const int t = wm * 64 + q * 16 + cl;
+      const int t = wn * 64 + q * 16 + cl;
+      const uint8_t* row = stg + G8_XT + t * 128;
+      const int sw = (t >> 1) & 7;
+      v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
+      v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
+      wo[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      const uint32_t b = sc[512 + (t >> 7) * 512 + (t & 31) * 16 + ((t & 127) >> 5) * 4 + g];
+      sw_[q] = vs ? b : 127u;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int t = wm * 64 + (2 * h + q) * 16 + cl;
         const uint8_t* row = stg + t * 128;
         const int sw = (t >> 1) & 7;
         v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
         v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
-        if (!v0) x0 = (v4i){0, 0, 0, 0};
-        if (!v1) x1 = (v4i){0, 0, 0, 0};
         ao[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        sa_[q] = vs ? stg[2 * G8_LDS_T + (t & 31) * 16 + (t >> 5) * 4 + g] : 127u;
+        const uint32_t b = sc[(t & 31) * 16 + (t >> 5) * 4 + g];
+        sa_[q] = vs ? b : 127u;
       }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[2 * h + q][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wo[j], ao[q], acc[2 * h + q][j], 0, 0, 0,
+                                                                                (int)sw_[j], 0, (int)sa_[q]);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wo[j], ao[i], acc[i][j], 0, 0, 0, (int)sw_[j], 0,
-                                                                      (int)sa_[i]);
   };
-
+  // k-tile kt: its requests landed for this wave once only tile kt+1's seven are outstanding; after the
+  // barrier every wave's have, and every wave is done reading tile kt-1, whose stage takes tile kt+2
+  // The loop runs in threes; past the last k-tile a step still waits, meets the barrier and issues its
+  // (clamped) requests, so that every path has the same request counts, and skips only the multiply.
+  auto step = [&](int kt, uint8_t* cur, uint8_t* refill) {
+    __builtin_amdgcn_sched_barrier(0);
+    WAIT_VMCNT(7);
+    // a bare barrier: __syncthreads() would add a workgroup fence, which waits for every request in
+    // flight (tile kt+1's too). The previous tile's LDS reads are complete: its MFMAs consumed them.
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    dma_tile(kt + 2, refill);
+    if (kt < KT) tile(cur, kt == KT - 1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
   dma_tile(0, st0);
-  for (int kt = 0; kt < KT; ++kt) {
-    uint8_t* cur = (kt & 1) ? st1 : st0;
-    uint8_t* nxt = (kt & 1) ? st0 : st1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      dma_tile(kt + 1, nxt);
-      WAIT_VMCNT(9);  // tile kt has landed for this wave (tile kt+1's nine requests may be in flight)
-    } else {
-      WAIT_VMCNT(0);
-    }
-    __syncthreads();  // ... and for every wave
-    tile(cur, !more);
-    __syncthreads();  // every read of `cur` is done before tile kt+2 lands in it
+  dma_tile(1, st1);
+  for (int kt = 0; kt < KT; kt += 3) {
+    step(kt, st0, st2);
+    step(kt + 1, st1, st0);
+    step(kt + 2, st2, st1);
   }
+  WAIT_VMCNT(0);  // the clamped re-reads land before the workgroup's LDS is released
 
   // lane (cl, g) of tile (i, j) holds n = n0 + wn*64 + 16j + 4g + (0..3) for m = m0 + wm*64 + 16i + cl
+  const int cl = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = m0 + wm * 64 + 16 * i + cl;
@@ -1313,6 +1372,7 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemm_mxfp8(const uint8
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + wn * 64 + 16 * j + 4 * g;
+      if (n >= N) continue;
       const v4f v = acc[i][j];
       uint16_t* dst = c + (int64_t)m * ldc + n;
       if (n + 3 < N && ((((uintptr_t)dst) & 7) == 0)) {

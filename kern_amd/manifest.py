@@ -161,8 +161,8 @@ def moe_finalize_rms(H: int, topk: int, eps: float = 1e-6) -> dict:
 def cublaslt_mxfp8_tn(n: int, rows_var: str = "tokens") -> dict:
     """The op of crates/kern-runtime/tests/mxfp8_gemm.rs:46-50 (params a, w, c, a_scale, w_scale, m, n, k),
     whose reference impl is the runtime built-in `extern:cublaslt_mxfp8_tn`, as a kernel launch of
-    kern_mx: grid [ceil(n/128), ceil(m/128)] with n a literal and m the var `rows_var` (a launch grid
-    reads vars, not params); c's row stride is n."""
+    kern_mx: grid [ceil(n/256), ceil(m/128)] of 512-thread workgroups with n a literal and m the var
+    `rows_var` (a launch grid reads vars, not params); c's row stride is n."""
     p = ["in buffer<fp8e4m3>", "in buffer<fp8e4m3>", "out buffer<bf16>", "in buffer<u8>", "in buffer<u8>",
          "i32", "i32", "i32"]
     return {
@@ -170,8 +170,8 @@ def cublaslt_mxfp8_tn(n: int, rows_var: str = "tokens") -> dict:
         "impl": {"launches": [{
             "module": MODULE, "entry": "kern_mx_gemm_mxfp8",
             "params": p + ["i32"],
-            "block": [256, 1, 1],
-            "grid": [_ceil(n, 128), {"ceil_div": [rows_var, 128]}, 1],
+            "block": [512, 1, 1],
+            "grid": [_ceil(n, 256), {"ceil_div": [rows_var, 128]}, 1],
             "args": [{"param": i} for i in range(8)] + [{"i32": n}],
         }]},
     }
