@@ -1065,14 +1065,19 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
   bmm_epilogue<MODE>(A, acc, 0, hw, nx, row0, valid, expert, lane);
 }
 
-// The MoE ops (moe_fc1 / moe_fc2): a persistent grid of one workgroup per CU. Each workgroup owns the
-// 256-row weight tiles lin = blockIdx.x + i * gridDim.x (i = 0, 1, ..; moe_tile with gx = m/256) of the live
-// slots. A pass classifies up to 512 of them at once (one per thread, one cta_limit read each) and
-// compacts the workgroup's tiles into two LDS lists: tiles of slots of more than skinny_rows rows run
-// on the LDS ring with all 8 waves, then the tiles of small slots run on the skinny path, the two halves
-// of the workgroup taking alternate ones without a barrier. The slot grows with i, so the pass whose
-// last candidate lies past the live slots is the last. Both kinds of tile share one launch, so a batch
-// that mixes small and large slots has one tail, and slots past num_non_exiting cost nothing.
+// The MoE ops (moe_fc1 / moe_fc2): a persistent grid of one workgroup per CU. Workgroup b owns the 256-row
+// weight tiles lin = b + i * G (i = 0, 1, ..; moe_tile with gx = m/256) of the live slots: those of slots
+// of more than skinny_rows rows run on the LDS ring with all 8 waves. The tiles of small slots run in
+// quarters (64 rows, one wave each, no LDS) that the eight waves take one each. In a launch with at most
+// 2G live tiles (a decode batch: T = 1 gives 128 FC1 tiles, which whole would leave half the CUs idle),
+// quarter o of a small tile owned by workgroup b' runs on workgroup b' + o*G/4, so that the few tiles
+// spread over every CU; otherwise a small tile's quarters all run on its owner. A pass classifies 128
+// candidate tiles of each owner (b alone, or b, b - G/4, b - G/2, b - 3G/4; one per thread, one
+// cta_limit read each) and compacts them into two LDS lists. The owners
+// are congruent mod 8, so along each owner's candidates the slot only grows: the pass whose last
+// candidate of the smallest owner lies past the live slots is the last. Both kinds of work share one
+// launch, so a batch that mixes small and large slots has one tail, and slots past num_non_exiting cost
+// nothing.
 template <int MODE>
 KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1080,12 +1085,25 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
   const int nne = min(A.num_non_exiting[0], A.max_slots);
   const int gx = A.m >> 8, G = gridDim.x;
   constexpr int kSkinny = skinny_rows<MODE>();
-  for (int base = 0;; base += 512) {
+  // quarter owners: b - o*G/4 (mod G) for o = 0..3 when the launch has at most 2G live tiles (and G/4 is a
+  // multiple of 8), else b for all four quarters. Spreading a large batch's small tiles cost more than it gained: config
+  // 4's FC1 (4096 tiles, half of them small) took 853 us against 712 us with each small tile's four
+  // quarters streaming together on its owner's CU (sharing the activation rows and DRAM pages).
+  const bool spread = (G & 31) == 0 && nne * gx <= 2 * G;
+  const int Q = G >> 2;
+  // the owner of quarter o's tiles (this workgroup itself when not spreading)
+  auto owner = [&](int o) { return spread ? (int)(((unsigned)blockIdx.x + (unsigned)(G - o * Q)) % (unsigned)G)
+                                          : (int)blockIdx.x; };
+  int bmin = owner(0);
+  for (int o = 1; o < 4; ++o) bmin = min(bmin, owner(o));
+  // thread (o, j): candidate j of quarter o's owner; a small tile there gives this workgroup quarter o
+  const int o = tid >> 7, j = tid & 127;
+  for (int base = 0;; base += 128) {
     int nx, slot;
-    moe_tile(blockIdx.x + G * (base + tid), gx, nx, slot);
+    moe_tile(owner(o) + G * (base + j), gx, nx, slot);
     const int v = slot < nne ? A.cta_limit[slot] - slot * BT : 0;
-    const bool ring = v > kSkinny, skin = v > 0 && v <= kSkinny;
-    __syncthreads();  // the previous pass's tiles are done with the lists and the LDS
+    const bool ring = o == 0 && v > kSkinny, skin = v > 0 && v <= kSkinny;
+    __syncthreads();  // the previous pass's work is done with the lists and the LDS
     const unsigned long long br = __ballot(ring), bs = __ballot(skin);
     if (lane == 0) wcnt[wave] = __popcll(br), wcnt[8 + wave] = __popcll(bs);
     __syncthreads();
@@ -1098,26 +1116,34 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
       ns += wcnt[8 + w];
     }
     const unsigned long long below = (1ull << lane) - 1ull;
-    if (ring) list[pr + __popcll(br & below)] = base + tid;
-    if (skin) list[512 + ps + __popcll(bs & below)] = base + tid;
-    // the pass's last candidate lies past the live slots: no later pass has work
-    moe_tile(blockIdx.x + G * (base + 511), gx, nx, slot);
+    if (ring) list[pr + __popcll(br & below)] = base + j;
+    if (spread) {
+      if (skin) list[512 + ps + __popcll(bs & below)] = (base + j) * 4 + o;
+    } else {
+      // all four thread groups classify the same tiles: quarter o of the r-th small tile goes to 4r + o,
+      // so that waves 0-3 take one tile's quarters together and waves 4-7 the next one's
+      const int r = ((wave & 1) ? wcnt[8 + wave - 1] : 0) + __popcll(bs & below);
+      if (skin) list[512 + 4 * r + o] = (base + j) * 4 + o;
+      ns = 4 * (wcnt[8] + wcnt[9]);
+    }
+    // the pass's last candidate of the smallest owner lies past the live slots: no later pass has work
+    moe_tile(bmin + G * (base + 127), gx, nx, slot);
     const bool last = slot >= nne;
     __syncthreads();
     for (int e = 0; e < nr; ++e) {
-      moe_tile(blockIdx.x + G * list[e], gx, nx, slot);
+      moe_tile(owner(0) + G * list[e], gx, nx, slot);
       const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
       if (e) __syncthreads();  // every wave's LDS reads and landing loads of the previous tile are done
       bmm_ring_tile<MODE>(A, L, nx, expert, row0, valid);
     }
-    const int half = wave >> 2, hw = wave & 3;
-    for (int e = half; e < ns; e += 2) {
-      moe_tile(blockIdx.x + G * list[512 + e], gx, nx, slot);
+    for (int e = wave; e < ns; e += 8) {
+      const int code = list[512 + e], q = code & 3;
+      moe_tile(owner(q) + G * (code >> 2), gx, nx, slot);
       const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
       if (kSkinny <= 16 || valid <= 16)
-        skinny_tile<MODE, 1>(A, nx, expert, row0, valid, hw, lane);
+        skinny_tile<MODE, 1>(A, nx, expert, row0, valid, q, lane);
       else
-        skinny_tile<MODE, (kSkinny + 15) / 16>(A, nx, expert, row0, valid, hw, lane);
+        skinny_tile<MODE, (kSkinny + 15) / 16>(A, nx, expert, row0, valid, q, lane);
     }
     if (last) break;
   }

@@ -214,8 +214,9 @@ def _route(ops, oracle, ids, local_start, local):
 
 # one persistent launch: slots of at most 16 routed rows (FC1; 8 for FC2) take the skinny path, the others
 # the LDS ring; decode-sized batches (all skinny), mixed ones and large ones (ring, ragged tails)
+# T = 1: eight single-row slots, every tile small, its quarters dealt out over all workgroups
 @pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 4096, 7168), (4, 256, 8, 4096, 7168),
-                                       (300, 8, 2, 512, 1024)])
+                                       (300, 8, 2, 512, 1024), (1, 256, 8, 4096, 7168)])
 def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
     _check_fc1(ops, oracle, wl.topk_ids(5 + T, T, E, k), E, m, K)
 
@@ -316,7 +317,7 @@ def _check_fc1(ops, oracle, ids, E, m, K):
 
 
 @pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 7168, 2048), (4, 256, 8, 7168, 2048),
-                                       (300, 8, 2, 512, 1024)])
+                                       (300, 8, 2, 512, 1024), (1, 256, 8, 7168, 2048)])
 def test_fc2_bf16(ops, oracle, T, E, k, m, K):
     _check_fc2(ops, oracle, wl.topk_ids(9 + T, T, E, k), E, m, K)
 
