@@ -421,7 +421,7 @@ KERN_DEV void gemv_rows_fixed(const uint16_t* __restrict__ x, const uint8_t* __r
   extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16_r##NKT(                                   \
       const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,          \
       uint16_t* __restrict__ y, int M, int N, int K) {                                                         \
-    gemv_rows_fixed<NKT>(x, w, wsf, y, M, N, K);                                                               \
+    gemv_rows_fixed<NKT>(x, w, wsf, y, M, N, K);                                                            \
   }
 GEMV_ROWS_FIXED(2)
 GEMV_ROWS_FIXED(4)
@@ -1069,7 +1069,7 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
 // weight tiles lin = b + i * G (i = 0, 1, ..; moe_tile with gx = m/256) of the live slots: those of slots
 // of more than skinny_rows rows run on the LDS ring with all 8 waves. The tiles of small slots run in
 // quarters (64 rows, one wave each, no LDS) that the eight waves take one each. In a launch with at most
-// 2G live tiles (a decode batch: T = 1 gives 128 FC1 tiles, which whole would leave half the CUs idle),
+// G/2 live tiles (a decode batch: T = 1 gives 128 FC1 tiles, which whole would leave half the CUs idle),
 // quarter o of a small tile owned by workgroup b' runs on workgroup b' + o*G/4, so that the few tiles
 // spread over every CU; otherwise a small tile's quarters all run on its owner. A pass classifies 128
 // candidate tiles of each owner (b alone, or b, b - G/4, b - G/2, b - 3G/4; one per thread, one
@@ -1085,11 +1085,13 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
   const int nne = min(A.num_non_exiting[0], A.max_slots);
   const int gx = A.m >> 8, G = gridDim.x;
   constexpr int kSkinny = skinny_rows<MODE>();
-  // quarter owners: b - o*G/4 (mod G) for o = 0..3 when the launch has at most 2G live tiles (and G/4 is a
-  // multiple of 8), else b for all four quarters. Spreading a large batch's small tiles cost more than it gained: config
-  // 4's FC1 (4096 tiles, half of them small) took 853 us against 712 us with each small tile's four
-  // quarters streaming together on its owner's CU (sharing the activation rows and DRAM pages).
-  const bool spread = (G & 31) == 0 && nne * gx <= 2 * G;
+  // quarter owners: b - o*G/4 (mod G) for o = 0..3 when the launch has at most G/2 live tiles (and G/4 is
+  // a multiple of 8), else b for all four quarters. Spreading the small tiles of larger launches cost
+  // more than it gained: config 4's FC1 (4096 tiles, half of them small) took 853 us against 712 us with
+  // each small tile's four quarters streaming together on its owner's CU (sharing the activation rows
+  // and DRAM pages), and a T = 1 FC2 (224 tiles) 17.8 us against 15.7 us; a T = 1 FC1 (128 tiles) gains,
+  // 27.7 us against 31.1 us.
+  const bool spread = (G & 31) == 0 && 2 * nne * gx <= G;
   const int Q = G >> 2;
   // the owner of quarter o's tiles (this workgroup itself when not spreading)
   auto owner = [&](int o) { return spread ? (int)(((unsigned)blockIdx.x + (unsigned)(G - o * Q)) % (unsigned)G)

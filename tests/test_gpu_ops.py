@@ -104,7 +104,9 @@ def test_repack_bitexact(ops, oracle, gated):
                                          (5, 256, 1536, 122, 132), (16, 512, 3072, 122, 132),
                                          (1, 512, 1024, 122, 132), (2, 1024, 2048, 122, 132),
                                          (1, 2048, 4096, 122, 132), (1, 7168, 8192, 122, 132),
-                                         (2, 112, 8192, 118, 136)])
+                                         (2, 112, 8192, 118, 136), (1, 9216, 7168, 122, 132),
+                                         (1, 16384, 2048, 122, 132), (2, 16384, 4096, 122, 132),
+                                         (1, 16384, 8192, 122, 132)])
 def test_gemv_w4a16(ops, oracle, M, N, K, lo, hi):
     x = wl.activations_bf16(100 + M, M, K)
     w, sf = wl.mxfp4_weights(200 + M, 1, N, K, lo, hi)
