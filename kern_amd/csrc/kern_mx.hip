@@ -729,8 +729,12 @@ KERN_DEV void moe_tile(int lin, int gx, int& nx, int& slot) {
 template <int MODE>
 KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int expert, int row0, int valid) {
   // the wave index through readfirstlane: provably uniform, so everything derived from it (the LDS
-  // bases of the direct loads) lives in scalar registers
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // bases of the direct loads) lives in scalar registers. The thread index goes through an opaque copy so
+  // that the lane-only addresses are derived anew in each tile: in the persistent MoE kernels they were
+  // hoisted out of the tile loop, spilled, and reloaded behind full memory waits in every tile.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wt = wave >> 2, wn = wave & 3;  // token half, weight quarter
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int m = A.m;
@@ -779,8 +783,8 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
   sx_step = A.sf_b_r128c4 ? 512 : 4;
 
   // requests (indices past the end are clamped to the last tile / group, whose data is then never
-  // multiplied): group 0 issues 4 per weight tile and 4 per weight-scale group, group 1 4 per activation
-  // tile and 2 per activation-scale group
+  // multiplied): group 0 issues 4 per weight tile and 4 per weight-scale group, group 1 NXR (at most 4)
+  // per activation tile and NXS (at most 2) per activation-scale group
   auto dma_w_tile = [&](int kt, uint8_t* sW) {
     kt = min(kt, KT - 1);
 #pragma unroll
@@ -797,15 +801,21 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       dma4(sbase + ((int64_t)f * KG + kg) * 256 + lane * 4, sSW + f * 256);
     }
   };
-  auto dma_x_tile = [&](int kt, uint8_t* sX) {
+  // group 1 requests only the 32-row blocks of the activation tile that hold live rows (NXR of 4), and the
+  // scale rows of the live 64-row halves (NXS of 2): LDS rows past them keep stale data that no wave reads
+  // (a wave reads the rows of its live 16-row subtiles only). A ring of 17-32-row slots (half of config 4's
+  // FC1 slots and most of its FC2 ones) thus issues 5 requests per k-tile instead of 8.
+  auto dma_x_tile = [&](int kt, uint8_t* sX, auto NXRc) {
+    constexpr int NXR = decltype(NXRc)::value;
     kt = min(kt, KT - 1);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dma16(xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
+    for (int r = 0; r < NXR; ++r) dma16(xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
   };
-  auto dma_x_scales = [&](int kg, uint8_t* sSX) {
+  auto dma_x_scales = [&](int kg, uint8_t* sSX, auto NXRc) {
+    constexpr int NXS = decltype(NXRc)::value > 2 ? 2 : 1;
     kg = min(kg, KG - 1);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) dma4(sx_row[h] + (int64_t)(kg * 4 + gw) * sx_step, sSX + 4 * (gw * BT + 64 * h));
+    for (int h = 0; h < NXS; ++h) dma4(sx_row[h] + (int64_t)(kg * 4 + gw) * sx_step, sSX + 4 * (gw * BT + 64 * h));
   };
 
   v4f acc[4][4];
@@ -818,28 +828,29 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
   const int live_ts = min(4, max(0, (valid - wt * 64 + 15) >> 4));
   const int c = lane & 15, g = lane >> 4;
 
-  // prologue: group 0 requests the weight scales of group 0 and weight tiles 0..3, group 1 the activation
-  // scales and activation tiles 0..2; tile 0 and the scales have landed once the later tiles' requests
-  // alone are outstanding
-  if (grp == 0) {
-    dma_w_scales(0, L.sw[0]);
-    dma_w_tile(0, L.w[0]);
-    dma_w_tile(1, L.w[1]);
-    dma_w_tile(2, L.w[2]);
-    dma_w_tile(3, L.w[3]);
-    WAIT_VMCNT(12);
-  } else {
-    dma_x_scales(0, L.sx[0]);
-    dma_x_tile(0, L.x[0]);
-    dma_x_tile(1, L.x[1]);
-    dma_x_tile(2, L.x[2]);
-    WAIT_VMCNT(8);
-  }
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-
-  auto run = [&](auto NTSc) {
+  auto run = [&](auto NTSc, auto NXRc) {
     constexpr int NTS = decltype(NTSc)::value;  // live token subtiles of this wave (uniform)
+    constexpr int NXR = decltype(NXRc)::value;  // live 32-row activation blocks (group 1's requests)
+    constexpr int NXS = NXR > 2 ? 2 : 1;        // activation-scale requests per k group
+    // prologue: group 0 requests the weight scales of group 0 and weight tiles 0..3, group 1 the activation
+    // scales and activation tiles 0..2; tile 0 and the scales have landed once the later tiles' requests
+    // alone are outstanding
+    if (grp == 0) {
+      dma_w_scales(0, L.sw[0]);
+      dma_w_tile(0, L.w[0]);
+      dma_w_tile(1, L.w[1]);
+      dma_w_tile(2, L.w[2]);
+      dma_w_tile(3, L.w[3]);
+      WAIT_VMCNT(12);
+    } else {
+      dma_x_scales(0, L.sx[0], NXRc);
+      dma_x_tile(0, L.x[0], NXRc);
+      dma_x_tile(1, L.x[1], NXRc);
+      dma_x_tile(2, L.x[2], NXRc);
+      WAIT_VMCNT(2 * NXR);
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     v4i wa[4];         // W operands of the tile in hand
     v8i xb[4];         // X operands, per token subtile
     uint32_t sxv[4];   // X scale bytes
@@ -905,13 +916,13 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       // first half-step: activation tile kt+3 into stage (kt+3)%4 (the next group's activation scales
       // first when kt+3 starts it), then this tile's operands, complete before the barrier because
       // group 0 refills the stage next
-      if (jt == 1) dma_x_scales(kg + 1, L.sx[sb ^ 1]);
-      dma_x_tile(kt + 3, L.x[st3]);
+      if (jt == 1) dma_x_scales(kg + 1, L.sx[sb ^ 1], NXRc);
+      dma_x_tile(kt + 3, L.x[st3], NXRc);
       read_tile(L.w[st], L.x[st], L.sw[sb], L.sx[sb], jt, jt == 0);
       WAIT_LGKMCNT0;
       // this wave's activations of tile kt+1 have landed once at most tiles kt+2, kt+3 and the scales
       // requested with them are outstanding
-      WAIT_VMCNT(8 + ((jt == 1 || jt == 2) ? 2 : 0));
+      WAIT_VMCNT(2 * NXR + ((jt == 1 || jt == 2) ? NXS : 0));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       // second half-step: multiply tile kt
@@ -940,12 +951,26 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       }
     }
   };
-  switch (live_ts) {
-    case 4: run(IC<4>{}); break;
-    case 3: run(IC<3>{}); break;
-    case 2: run(IC<2>{}); break;
-    case 1: run(IC<1>{}); break;
-    default: run(IC<0>{}); break;
+  // group 0 (weights, token rows 0-63) by its live subtiles; group 1 (activations, rows 64-127) by its live
+  // subtiles and the live 32-row blocks it requests, which valid fixes together: 1-32 rows (0, 1),
+  // 33-64 (0, 2), 65-80 (1, 3), 81-96 (2, 3), 97-112 (3, 4), 113-128 (4, 4)
+  if (grp == 0) {
+    switch (live_ts) {
+      case 4: run(IC<4>{}, IC<4>{}); break;
+      case 3: run(IC<3>{}, IC<4>{}); break;
+      case 2: run(IC<2>{}, IC<4>{}); break;
+      case 1: run(IC<1>{}, IC<4>{}); break;
+      default: run(IC<0>{}, IC<4>{}); break;
+    }
+  } else {
+    switch (min(4, max(1, (valid + 31) >> 5)) * 8 + live_ts) {
+      case 1 * 8 + 0: run(IC<0>{}, IC<1>{}); break;
+      case 2 * 8 + 0: run(IC<0>{}, IC<2>{}); break;
+      case 3 * 8 + 1: run(IC<1>{}, IC<3>{}); break;
+      case 3 * 8 + 2: run(IC<2>{}, IC<3>{}); break;
+      case 4 * 8 + 3: run(IC<3>{}, IC<4>{}); break;
+      default: run(IC<4>{}, IC<4>{}); break;  // 113-128 rows (and any count past a full tile)
+    }
   }
   // the ring's last requests (clamped re-reads) must land before the workgroup's LDS is released
   WAIT_VMCNT(0);
@@ -978,6 +1003,8 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
 // independently, so one half's start and end overlap the other's streaming.
 template <int MODE, int NTS>
 KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int valid, int hw, int lane) {
+  // lane-only addresses derived anew in each tile (an opaque copy of the lane index), as in bmm_ring_tile
+  asm volatile("" : "+v"(lane));
   const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
   const int c = lane & 15, g = lane >> 4;
   const int rg0 = (nx * BN) >> 4;
@@ -1098,9 +1125,14 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
                                           : (int)blockIdx.x; };
   int bmin = owner(0);
   for (int o = 1; o < 4; ++o) bmin = min(bmin, owner(o));
-  // thread (o, j): candidate j of quarter o's owner; a small tile there gives this workgroup quarter o
-  const int o = tid >> 7, j = tid & 127;
   for (int base = 0;; base += 128) {
+    // thread (o, j): candidate j of quarter o's owner; a small tile there gives this workgroup quarter o.
+    // These lane values are derived anew in each pass from an opaque copy of the thread index: hoisted out
+    // of the loop they stay live across the tiles, which need every register, and were spilled to scratch
+    // and reloaded behind full memory waits in every pass.
+    int tp = tid;
+    asm volatile("" : "+v"(tp));
+    const int o = tp >> 7, j = tp & 127;
     int nx, slot;
     moe_tile(owner(o) + G * (base + j), gx, nx, slot);
     const int v = slot < nne ? A.cta_limit[slot] - slot * BT : 0;
@@ -1117,7 +1149,7 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
       nr += wcnt[w];
       ns += wcnt[8 + w];
     }
-    const unsigned long long below = (1ull << lane) - 1ull;
+    const unsigned long long below = (1ull << (tp & 63)) - 1ull;
     if (ring) list[pr + __popcll(br & below)] = base + j;
     if (spread) {
       if (skin) list[512 + ps + __popcll(bs & below)] = (base + j) * 4 + o;
