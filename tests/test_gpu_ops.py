@@ -149,9 +149,12 @@ def test_gemm_closed_form_kat(ops):
 
 # --------------------------------------------------------------------------------------- dense e4m3 (config 3 mode)
 
-# small M (one live 16-row subtile, or one and a row), ragged M, K not a multiple of 1024
+# small M (one live 16-row subtile, or one and a row), ragged M, K not a multiple of 1024; the last 128-row
+# tile of 20, 40, 70, 90, 100 and 120 rows: the activation loader's six (live subtiles, live 32-row
+# request blocks) cases, (0, 1) (0, 2) (1, 3) (2, 3) (3, 4) (4, 4) for its rows 64-127
 @pytest.mark.parametrize("M,m,k", [(300, 512, 1024), (4096, 2048, 7168), (5, 512, 1024), (16, 2048, 7168),
-                                   (17, 512, 1536)])
+                                   (17, 512, 1536), (148, 512, 1024), (168, 512, 1024), (198, 512, 1024),
+                                   (218, 512, 1024), (228, 512, 1024), (248, 512, 1024)])
 def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
     x = wl.activations_bf16(31, M, k, outlier_frac=0.01)
     w, sf = wl.mxfp4_weights(32, 1, m, k, 122, 132)
@@ -239,6 +242,23 @@ def test_fc_split_batch(ops, oracle):
     print("[fc split] 64 experts, one slot of 41 rows", flush=True)
     _check_fc1(ops, oracle, ids, 64, 512, 1024)
     _check_fc2(ops, oracle, ids, 64, 512, 1024)
+
+
+def _ring_row_ids():
+    """440 tokens, top-2 over 8 experts: experts 0-5 take 20, 40, 70, 90, 100 and 120 rows (first choice), expert
+    6 every token's second choice (three full 128-row slots and one of 56); expert 7 none. Every slot takes the
+    LDS ring, and each of its activation loader's (live subtiles, live 32-row blocks) cases occurs."""
+    sizes = [20, 40, 70, 90, 100, 120]
+    first = np.repeat(np.arange(len(sizes), dtype=np.int32), sizes)
+    ids = np.stack([first, np.full_like(first, 6)], axis=1)
+    return ids[np.random.default_rng(3).permutation(len(first))]
+
+
+def test_fc_ring_row_counts(ops, oracle):
+    ids = _ring_row_ids()
+    print("[fc ring rows] slots of 20..128 rows", flush=True)
+    _check_fc1(ops, oracle, ids, 8, 512, 1024)
+    _check_fc2(ops, oracle, ids, 8, 512, 1024)
 
 
 def test_fc2_live_count_is_capped_by_the_tables(ops, oracle):
