@@ -1366,6 +1366,24 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8
     asm volatile("" : "+v"(cl), "+v"(g));
     const int kr = K & 127;  // valid bytes of a partial last tile (its chunks past K are zeros)
     const bool vs = !last || kr == 0 || 32 * g < kr;  // this lane's k block lies within K
+    // Scales (R128c4: row t's four k blocks are one dword at (t & 31) * 16 + ((t & 127) >> 5) * 4 of its
+    // 128-row block). The dwords of subtiles q and q + 2 (rows 32 apart) are neighbours, so one 8-byte read
+    // fetches both, and the lane takes its k block's byte by a shift. Lanes that differ only in their k block
+    // read the same 8 bytes. A read per byte cost the LDS as much as a 16-byte read, and conflicted.
+    const int sh = 8 * g;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint2 d = *reinterpret_cast<const uint2*>(sc + 512 + (wn >> 1) * 512 + (q * 16 + cl) * 16 + 8 * (wn & 1));
+      sw_[q] = vs ? (d.x >> sh) & 255u : 127u;
+      sw_[q + 2] = vs ? (d.y >> sh) & 255u : 127u;
+    }
+    uint32_t sa4[2][2];  // [half][subtile]: rows wm*64 + (2h + q)*16 + cl
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint2 d = *reinterpret_cast<const uint2*>(sc + (q * 16 + cl) * 16 + 8 * wm);
+      sa4[0][q] = vs ? (d.x >> sh) & 255u : 127u;
+      sa4[1][q] = vs ? (d.y >> sh) & 255u : 127u;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int t = wn * 64 + q * 16 + cl;
@@ -1374,8 +1392,6 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8
       v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
       v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
       wo[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      const uint32_t b = sc[512 + (t >> 7) * 512 + (t & 31) * 16 + ((t & 127) >> 5) * 4 + g];
-      sw_[q] = vs ? b : 127u;
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -1388,8 +1404,7 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8
         v4i x0 = *reinterpret_cast<const v4i*>(row + ((g ^ sw) << 4));
         v4i x1 = *reinterpret_cast<const v4i*>(row + (((g + 4) ^ sw) << 4));
         ao[q] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        const uint32_t b = sc[(t & 31) * 16 + (t >> 5) * 4 + g];
-        sa_[q] = vs ? b : 127u;
+        sa_[q] = sa4[h][q];
       }
 #pragma unroll
       for (int q = 0; q < 2; ++q)
