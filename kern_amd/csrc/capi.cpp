@@ -343,7 +343,7 @@ extern "C" int kern_moe_quant(const void* x, void* q, void* sf, int32_t tokens, 
           tokens);
   if (tokens == 0) return KERN_OK;
   REQUIRE(x && q && sf, "moe_quant: null buffer");
-  const int64_t chunks = (int64_t)tokens * (K / 8);  // one lane per 8 elements
+  const int64_t chunks = (int64_t)tokens * (K / 8);  // 8-element chunks; a workgroup takes 512 (16 elements a lane)
   REQUIRE((chunks + 511) / 512 < (int64_t)1 << 31, "moe_quant: %lld elements exceed the grid",
           (long long)chunks * 8);
   Args a;

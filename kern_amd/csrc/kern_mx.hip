@@ -20,37 +20,36 @@ struct IC { static constexpr int value = V; };
 
 // ====================================================================================== quantizer
 // op moe_quant (fixtures/k3/head.json:25057): in bf16 x[T][K], out u8 q[T][K], out u8 sf[T][K/32], i32 T,
-// launch i32 K. Four lanes per 32-element block, 8 elements (16 bytes) per lane, so every wave-wide
-// load covers 1 KiB of contiguous input and every store 512 contiguous bytes; the block amax is
-// reduced over the lane quad with DPP. Each lane handles chunks i and i + 256 of its workgroup's 512
-// (both loads in flight together). Grid ceil(T*K/8 / 512), block 256.
+// launch i32 K. Two lanes per 32-element block, 16 elements (two 16-byte loads) per lane, so a wave-wide
+// load covers 1 KiB of contiguous input and each 16-byte store 1 KiB of output; the block amax is
+// reduced over the lane pair with DPP. A workgroup covers 4096 elements: grid ceil(T*K / 4096), block 256.
 extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint16_t* __restrict__ x,
                                                                      uint8_t* __restrict__ q,
                                                                      uint8_t* __restrict__ sf, int T, int K) {
-  const int64_t i0 = (int64_t)blockIdx.x * 512 + threadIdx.x;  // 8-element chunk
-  const int64_t n = (int64_t)T * (K >> 3);
-  // a lane quad is in or out of range together (n is a multiple of 4)
-  v4u v[2];
+  // a lane takes 16 adjacent elements (half a 32-element block), a lane pair one block: one cross-lane step
+  // for the block's amax, one 16-byte store. (8 elements per lane, four lanes per block, two chunks per
+  // lane: 3% slower at config 3's activations; more than one pair per lane was slower still.)
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t np = (int64_t)T * (K >> 4);
+  // a lane pair is in or out of range together (K % 32 == 0: np is even)
+  if (p >= np) return;
+  const v4u v0 = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(x) + 2 * p);
+  const v4u v1 = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(x) + 2 * p + 1);
+  uint32_t amax = 0;
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-    if (i0 + 256 * h < n) v[h] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(x) + i0 + 256 * h);
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int64_t i = i0 + 256 * h;
-    if (i < n) {
-      uint32_t amax = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) amax = max(amax, max((v[h][j] << 16) & 0x7fffffffu, v[h][j] & 0x7fff0000u));
-      amax = max(amax, (uint32_t)__builtin_amdgcn_mov_dpp((int)amax, 0xB1, 0xF, 0xF, false));  // lane ^ 1
-      amax = max(amax, (uint32_t)__builtin_amdgcn_mov_dpp((int)amax, 0x4E, 0xF, 0xF, false));  // lane ^ 2
-      const uint32_t sc = mx_scale_code(amax);
-      uint2 out;
-      out.x = mx_pack4(v[h][0], v[h][1], sc);
-      out.y = mx_pack4(v[h][2], v[h][3], sc);
-      reinterpret_cast<uint2*>(q)[i] = out;
-      if ((threadIdx.x & 3) == 0) sf[i >> 2] = (uint8_t)sc;
-    }
+  for (int j = 0; j < 4; ++j) {
+    amax = max(amax, max((v0[j] << 16) & 0x7fffffffu, v0[j] & 0x7fff0000u));
+    amax = max(amax, max((v1[j] << 16) & 0x7fffffffu, v1[j] & 0x7fff0000u));
   }
+  amax = max(amax, (uint32_t)__builtin_amdgcn_mov_dpp((int)amax, 0xB1, 0xF, 0xF, false));  // lane ^ 1
+  const uint32_t sc = mx_scale_code(amax);
+  v4u out;
+  out[0] = mx_pack4(v0[0], v0[1], sc);
+  out[1] = mx_pack4(v0[2], v0[3], sc);
+  out[2] = mx_pack4(v1[0], v1[1], sc);
+  out[3] = mx_pack4(v1[2], v1[3], sc);
+  reinterpret_cast<v4u*>(q)[p] = out;
+  if ((threadIdx.x & 1) == 0) sf[p >> 1] = (uint8_t)sc;
 }
 
 // ====================================================================================== repack

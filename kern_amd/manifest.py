@@ -27,7 +27,7 @@ def _ceil(a: int, b: int) -> int:
 
 def moe_quant(K: int) -> dict:
     """moe_quant(in bf16 x[T][K], out u8 q[T][K], out u8 sf[T][K/32], i32 T); launch adds i32 K.
-    A 256-thread workgroup covers 512 chunks of 8 elements: grid ceil(T*K/8 / 512)."""
+    A 256-thread workgroup covers 4096 elements (16 per lane): grid ceil(T*K/8 / 512) = ceil(T*K / 4096)."""
     assert K % 32 == 0
     return {
         "params": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32"],
