@@ -765,21 +765,25 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
     const int t = 32 * r + 8 * gw + (lane >> 3);
     xsrc[r] = A.b + token_of(t) * K + ((xpos ^ ((t >> 1) & 7)) << 4);
   }
-  // group 1: activation scale dwords, rows 64h + lane of k-tile gw of a group; address of k-tile 0's dword
-  // and the step between k-tiles: linear [T][K/32] or R128c4 (one 512-byte tile per 128 rows x 4 k blocks)
+  // group 1: activation scale dwords of a k group, gathered into LDS as [tile row][k-tile of the group] (16
+  // bytes a row): request h of wave gw fills rows 16*(4h + gw) + lane/4, k-tile lane % 4, so that the
+  // multiplying waves read a row's four k-tiles in one 16-byte read per group instead of one byte read
+  // per k-tile (a k-tile's scale dword holds the row's four 32-wide k blocks). sx_step: between k-tiles,
+  // linear [T][K/32] or R128c4 (one 512-byte tile per 128 rows x 4 k blocks)
+  const int sx_step = A.sf_b_r128c4 ? 512 : 4;
   const uint8_t* sx_row[2];
-  int sx_step;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int64_t srow = token_of(64 * h + lane);
+    const int64_t srow = token_of(16 * (4 * h + gw) + (lane >> 2));
+    const uint8_t* base;
     if (A.sf_b_r128c4) {
       const int64_t kb4 = K >> 7;  // ceil(kblocks/4) with K % 128 == 0
-      sx_row[h] = A.sf_b + 512 * ((srow >> 7) * kb4) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
+      base = A.sf_b + 512 * ((srow >> 7) * kb4) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
     } else {
-      sx_row[h] = A.sf_b + srow * (K >> 5);
+      base = A.sf_b + srow * (K >> 5);
     }
+    sx_row[h] = base + (lane & 3) * sx_step;
   }
-  sx_step = A.sf_b_r128c4 ? 512 : 4;
 
   // requests (indices past the end are clamped to the last tile / group, whose data is then never
   // multiplied): group 0 issues 4 per weight tile and 4 per weight-scale group, group 1 NXR (at most 4)
@@ -814,7 +818,7 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
     constexpr int NXS = decltype(NXRc)::value > 2 ? 2 : 1;
     kg = min(kg, KG - 1);
 #pragma unroll
-    for (int h = 0; h < NXS; ++h) dma4(sx_row[h] + (int64_t)(kg * 4 + gw) * sx_step, sSX + 4 * (gw * BT + 64 * h));
+    for (int h = 0; h < NXS; ++h) dma4(sx_row[h] + (int64_t)(kg * 4) * sx_step, sSX + 256 * (4 * h + gw));
   };
 
   v4f acc[4][4];
@@ -852,7 +856,7 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
     __builtin_amdgcn_sched_barrier(0);
     v4i wa[4];         // W operands of the tile in hand
     v8i xb[4];         // X operands, per token subtile
-    uint32_t sxv[4];   // X scale bytes
+    v4u sxq[4];        // X scale dwords of the current k group (k-tile j in sxq[ts][j])
     uint32_t swd[4];   // weight-scale dwords of the current k group
     // operands of the tile in stage st (k-tile jt of its group; weight scales too when jt == 0)
     auto read_tile = [&](const uint8_t* sW, const uint8_t* sX, const uint8_t* sSW, const uint8_t* sSX, int jt,
@@ -871,20 +875,22 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
         const v4i x0 = *reinterpret_cast<const v4i*>(xr + ((g ^ sw) << 4));
         const v4i x1 = *reinterpret_cast<const v4i*>(xr + (((g + 4) ^ sw) << 4));
         xb[ts] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        // the scale byte of this lane's 32-wide k block, read as a byte so that no shift waits on it
-        sxv[ts] = sSX[(jt * BT + t) * 4 + g];
+        // the row's scale dwords for the group's four k-tiles, at its first
+        if (jt == 0) sxq[ts] = *reinterpret_cast<const v4u*>(sSX + t * 16);
       }
     };
     auto mfmas = [&](auto Jt) {
       constexpr int jt = decltype(Jt)::value;  // k-tile within the group: scale byte of the weights
 #pragma unroll
-      for (int ts = 0; ts < NTS; ++ts)
+      for (int ts = 0; ts < NTS; ++ts) {
+        const uint32_t sxb = sxq[ts][jt] >> (8 * g);  // this lane's k block's byte, in byte 0
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs) {
           const v8i wb = {wa[rs][0], wa[rs][1], wa[rs][2], wa[rs][3], 0, 0, 0, 0};
           acc[ts][rs] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wb, xb[ts], acc[ts][rs], 4, 0, jt,
-                                                                          (int)swd[rs], 0, (int)sxv[ts]);
+                                                                          (int)swd[rs], 0, (int)sxb);
         }
+      }
     };
     // k-tile t = 8*kk + J lives in stage J % 4; its group's scales in slot J / 4 (group parity)
     auto step0 = [&](int kk, auto Jc) {  // group 0
