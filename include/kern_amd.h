@@ -211,6 +211,12 @@ int kern_mx_module(kern_module* out);
  * K % 32 == 0. */
 int kern_moe_quant(const void* x, void* q, void* sf, int32_t tokens, int32_t K, void* stream);
 
+/* f32 -> MXFP8 with the FC1 epilogue's codec (the MXFP8 output stage of trtllm_bmm_mxe4m3_mxe2m1_mxe4m3,
+ * head.json:25459, whose sf_c rule is probe.py:38-43's): in f32 x[T][K], out u8 q[T][K] (e4m3), out u8
+ * sf[T][K/32] (ue8m0, linear); same scale and element rules as kern_moe_quant, applied to f32 values
+ * (an f32 subnormal or a value between bf16 neighbours is encoded from its exact value). K % 32 == 0. */
+int kern_mxfp8_quant_f32(const float* x, void* q, void* sf, int32_t tokens, int32_t K, void* stream);
+
 /* k3_moe_w_shuffle (head.json:26358; derive program head.json:28670): in u8 raw [E][rows][row_bytes],
  * out u8 repacked (same size), i32 rows, i32 row_bytes, i32 gated; launch i32 E.
  * rows % 16 == 0, row_bytes % 256 == 0 (K % 512 == 0). */

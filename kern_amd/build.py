@@ -25,13 +25,16 @@ HSACO = os.path.join(LIBDIR, "kern_mx.hsaco")
 LIB = os.path.join(LIBDIR, "libkern_amd.so")
 ARCH = "gfx950"
 
-# hipcc flags for device code: packed-fp32 VALU ops stay off (they have given wrong results on these boxes)
+# hipcc flags for device code: packed-fp32 VALU ops stay off (they have given wrong results on these boxes).
+# -cuid fixes the compilation-unit id, which hipcc otherwise derives from the source and output paths: with
+# it the code object, and so its pinned sha256, is the same in every checkout.
 DEVICE_FLAGS = ["-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-                "-packed-fp32-ops"]
+                "-packed-fp32-ops", "-cuid=kern_mx"]
 
 ENTRIES = {
     # entry: (launch params as the op JSON in kernel_index/ declares them)
     "kern_mx_quant_bf16": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "i32"],
+    "kern_mx_quant_f32": ["in buffer<f32>", "out buffer<u8>", "out buffer<u8>", "i32", "i32"],
     "kern_mx_w_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
     "kern_mx_sf_shuffle": ["in buffer<u8>", "out buffer<u8>", "i32", "i32", "i32", "i32"],
     "kern_mx_gemv_bf16": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "i32", "i32",
@@ -81,14 +84,24 @@ def _run(cmd):
     return out
 
 
-def build_code_object() -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
-    tmp = HSACO + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", "--no-gpu-bundle-output", *DEVICE_FLAGS, os.path.join(CSRC, "kern_mx.hip"),
-          "-o", tmp])
-    os.replace(tmp, HSACO)
-    with open(HSACO, "rb") as f:
+def build_code_object(csrc: str = CSRC, out: str = HSACO) -> str:
+    """Compile csrc/kern_mx.hip to `out`; returns its sha256 (the same for any csrc and out paths)."""
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", "--no-gpu-bundle-output", *DEVICE_FLAGS,
+          os.path.join(csrc, "kern_mx.hip"), "-o", tmp])
+    os.replace(tmp, out)
+    with open(out, "rb") as f:
         return hashlib.sha256(f.read()).hexdigest()
+
+
+def pinned_sha256() -> str:
+    """The sha256 kernel_index/kern_mx.toml pins."""
+    with open(os.path.join(ROOT, "kernel_index", "kern_mx.toml")) as f:
+        for line in f:
+            if line.startswith("sha256 = "):
+                return line.split('"')[1]
+    raise RuntimeError("kernel_index/kern_mx.toml has no sha256")
 
 
 def build_library(sha: str) -> None:

@@ -351,6 +351,19 @@ extern "C" int kern_moe_quant(const void* x, void* q, void* sf, int32_t tokens, 
   return launch("kern_mx_quant_bf16", (uint32_t)((chunks + 511) / 512), 1, 1, 256, stream, a);
 }
 
+extern "C" int kern_mxfp8_quant_f32(const float* x, void* q, void* sf, int32_t tokens, int32_t K, void* stream) {
+  REQUIRE(tokens >= 0 && K > 0 && K % 32 == 0, "mxfp8_quant_f32: need K %% 32 == 0 and tokens >= 0 (K=%d tokens=%d)",
+          K, tokens);
+  if (tokens == 0) return KERN_OK;
+  REQUIRE(x && q && sf, "mxfp8_quant_f32: null buffer");
+  const int64_t pieces = (int64_t)tokens * (K / 8);  // 8-element pieces, one a lane
+  REQUIRE((pieces + 255) / 256 < (int64_t)1 << 31, "mxfp8_quant_f32: %lld elements exceed the grid",
+          (long long)pieces * 8);
+  Args a;
+  a.put(x), a.put(q), a.put(sf), a.put(tokens), a.put(K);
+  return launch("kern_mx_quant_f32", (uint32_t)((pieces + 255) / 256), 1, 1, 256, stream, a);
+}
+
 extern "C" int kern_moe_w_shuffle(const void* raw, void* out, int32_t experts, int32_t rows, int32_t row_bytes,
                                   int32_t gated, void* stream) {
   REQUIRE(experts > 0 && rows > 0 && rows % 16 == 0 && row_bytes > 0 && row_bytes % 256 == 0,

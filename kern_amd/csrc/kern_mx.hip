@@ -52,6 +52,33 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint1
   if ((threadIdx.x & 1) == 0) sf[p >> 1] = (uint8_t)sc;
 }
 
+// f32 -> MXFP8 with the codec of the FC1 epilogue (mx_scale_code of the block's largest |bits|, then
+// mx_code2 pairs): in f32 x[T][K], out u8 q[T][K], out u8 sf[T][K/32], i32 T, i32 K (K % 32 == 0). Four
+// lanes per 32-element block, eight elements (two 16-byte loads) per lane; the block amax is reduced over
+// the four lanes. Grid ceil(T*K / 2048), block 256.
+extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_f32(const float* __restrict__ x,
+                                                                    uint8_t* __restrict__ q,
+                                                                    uint8_t* __restrict__ sf, int T, int K) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 8-element piece
+  const int64_t np = (int64_t)T * (K >> 3);
+  // the four lanes of a block are in or out of range together (K % 32 == 0: np is a multiple of 4)
+  if (p >= np) return;
+  const v4u v0 = reinterpret_cast<const v4u*>(x)[2 * p];
+  const v4u v1 = reinterpret_cast<const v4u*>(x)[2 * p + 1];
+  uint32_t amax = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) amax = max(amax, max(v0[j] & 0x7fffffffu, v1[j] & 0x7fffffffu));
+  amax = max(amax, (uint32_t)__shfl_xor((int)amax, 1));
+  amax = max(amax, (uint32_t)__shfl_xor((int)amax, 2));
+  const uint32_t sc = mx_scale_code(amax);
+  const uint32_t c0 = mx_code2(__uint_as_float(v0[0]), __uint_as_float(v0[1]), sc);
+  const uint32_t c1 = mx_code2(__uint_as_float(v0[2]), __uint_as_float(v0[3]), sc);
+  const uint32_t c2 = mx_code2(__uint_as_float(v1[0]), __uint_as_float(v1[1]), sc);
+  const uint32_t c3 = mx_code2(__uint_as_float(v1[2]), __uint_as_float(v1[3]), sc);
+  reinterpret_cast<uint2*>(q)[p] = make_uint2(c0 | (c1 << 16), c2 | (c3 << 16));
+  if ((threadIdx.x & 3) == 0) sf[p >> 2] = (uint8_t)sc;
+}
+
 // ====================================================================================== repack
 // derive op k3_moe_w_shuffle (head.json:26358): in u8 raw, out u8 shuffled, i32 rows, i32 row_bytes,
 // i32 gated; launch prepends i32 E. One thread per 16-byte lane slot of the output; grid
@@ -158,10 +185,12 @@ KERN_DEV v4f gemv_rows(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr_, __
       }
     }
     if (s0 == 0) {
+      // per lane: the scale region holds exactly spieces pieces (K/2 bytes), which need not fill a
+      // wave's request, and lanes past it must not write LDS beyond the region
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int q0 = 256 * r + 64 * wave;
-        if (q0 < spieces) dma16_buf(sr_, (q0 + lane) * 16, ss + q0 * 16);
+        if (q0 + lane < spieces) dma16_buf(sr_, (q0 + lane) * 16, ss + q0 * 16);
       }
     }
     for (int i0 = s0; i0 < s0 + sb; i0 += NB) {

@@ -39,6 +39,7 @@ I64 = ctypes.c_int64
 
 _SIGS = {
     "kern_moe_quant": [P, P, P, I32, I32, P],
+    "kern_mxfp8_quant_f32": [P, P, P, I32, I32, P],
     "kern_moe_w_shuffle": [P, P, I32, I32, I32, I32, P],
     "kern_moe_sf_shuffle": [P, P, I32, I32, I32, I32, P],
     "kern_moe_routing": [P] * 8 + [I32] * 4 + [P],
@@ -160,6 +161,12 @@ def moe_quant(x, q, sf, tokens, *, K):
     """moe_quant(in bf16 x[T,K], out u8 q[T,K], out u8 sf[T,K/32], i32 tokens) — head.json:25057."""
     check(lib().kern_moe_quant(_ptr(x, "x", bf16, tokens * K), _ptr(q, "q", u8, tokens * K),
                                _ptr(sf, "sf", u8, tokens * K // 32), tokens, K, _stream()))
+
+
+def mxfp8_quant_f32(x, q, sf, tokens, *, K):
+    """f32 [T,K] -> MXFP8 codes u8 [T,K] and ue8m0 scales u8 [T,K/32] with the FC1 epilogue's codec."""
+    check(lib().kern_mxfp8_quant_f32(_ptr(x, "x", f32, tokens * K), _ptr(q, "q", u8, tokens * K),
+                                     _ptr(sf, "sf", u8, tokens * K // 32), tokens, K, _stream()))
 
 
 def k3_moe_w_shuffle(raw, out, rows, row_bytes, gated, *, experts):

@@ -128,3 +128,58 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_code_object_build_is_path_independent(tmp_path):
+    """The pin is reproducible: kern_mx.hip built from a copy of the sources in another directory, to
+    another output path, hashes to the sha256 kernel_index/kern_mx.toml pins (hipcc's compilation-unit
+    id would otherwise follow the paths)."""
+    import shutil
+
+    src = tmp_path / "elsewhere" / "csrc"
+    shutil.copytree(kb.CSRC, src)
+    sha = kb.build_code_object(str(src), str(tmp_path / "out" / "copy.hsaco"))
+    assert sha == kb.pinned_sha256()
+
+
+_FUZZ = r"""
+import ctypes, random, sys
+L = ctypes.CDLL(sys.argv[1])
+img = open(sys.argv[2], "rb").read()
+sizes = (ctypes.c_uint32 * 64)()
+n = ctypes.c_int()
+def call(b):
+    rc = L.kern_code_object_param_sizes(b, len(b), b"kern_mx_quant_bf16", sizes, 64, ctypes.byref(n))
+    assert rc in (0, 2), rc
+    return rc
+assert call(img) == 0
+note = img.find(b"AMDGPU")  # the metadata note's name; its msgpack follows
+assert note > 0
+rng = random.Random(5)
+for cut in list(range(0, 256)) + [note + d for d in range(-16, 4096, 7)] + [len(img) - d for d in range(1, 64)]:
+    call(img[:max(0, cut)])
+for _ in range(3000):
+    b = bytearray(img)
+    for _ in range(rng.randint(1, 4)):
+        at = rng.randrange(note, min(len(b), note + 60000)) if rng.random() < 0.9 else rng.randrange(64)
+        b[at] = rng.choice([0xc4, 0xc5, 0xc6, 0xdb, 0xdd, 0xdf, 0xff, 0x00, rng.randrange(256)])
+    call(bytes(b))
+# section header fields pushed to the edge of 64-bit range
+for off, val in [(0x28, 2**64 - 8), (0x28, len(img)), (0x3a, 0), (0x3c, 0xffff)]:
+    b = bytearray(img)
+    b[off:off + (8 if off == 0x28 else 2)] = val.to_bytes(8 if off == 0x28 else 2, "little")
+    call(bytes(b))
+print("ok")
+"""
+
+
+def test_metadata_parser_survives_corrupt_images(lib, tmp_path):
+    """kern_code_object_param_sizes parses caller-supplied images: truncated ones, corrupted msgpack lengths
+    (bin/str/array/map sizes far past the data) and section headers at the edge of the 64-bit range are
+    refused with KERN_ERR_KERNEL_ARTIFACT, never read past the image (run in a child process, so an
+    out-of-bounds read would show as a crash here rather than end the test session)."""
+    script = tmp_path / "fuzz.py"
+    script.write_text(_FUZZ)
+    r = subprocess.run([sys.executable, str(script), ops.LIB_PATH, ops.HSACO_PATH], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout[-500:], r.stderr[-2000:])

@@ -106,7 +106,8 @@ def test_repack_bitexact(ops, oracle, gated):
                                          (1, 2048, 4096, 122, 132), (1, 7168, 8192, 122, 132),
                                          (2, 112, 8192, 118, 136), (1, 9216, 7168, 122, 132),
                                          (1, 16384, 2048, 122, 132), (2, 16384, 4096, 122, 132),
-                                         (1, 16384, 8192, 122, 132)])
+                                         (1, 16384, 8192, 122, 132), (4, 512, 512, 122, 132),
+                                         (16, 48, 512, 118, 136), (3, 64, 1536, 122, 132)])
 def test_gemv_w4a16(ops, oracle, M, N, K, lo, hi):
     x = wl.activations_bf16(100 + M, M, K)
     w, sf = wl.mxfp4_weights(200 + M, 1, N, K, lo, hi)
@@ -168,10 +169,10 @@ def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
     ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c, ds, M=M, m=m, k=k, dbg=dbg)
     _sync()
     acc = to_np(dbg)
-    rows = slice(None) if M <= 512 else np.r_[0:128, 1900:2000, M - 70:M]
     qn, qsn = to_np(q), to_np(qs)
-    ref_c, ref_acc = oracle.gemm_e4m3_pt(to_np(wp), to_np(sfp), qn[rows], qsn[rows], m, k, d_scale)
-    assert_gemm_close(acc[rows], ref_acc, "prefill acc")
+    # every row (config 3: 4096 x 2048 x 7168 takes the threaded oracle a few seconds)
+    ref_c, ref_acc = oracle.gemm_e4m3_pt(to_np(wp), to_np(sfp), qn, qsn, m, k, d_scale)
+    assert_gemm_close(acc, ref_acc, "prefill acc")
     # the epilogue cast is bit-exact given the kernel's own accumulator
     np.testing.assert_array_equal(to_np(c), oracle.e4m3_from_f32(acc * np.float32(d_scale)))
 
@@ -221,9 +222,23 @@ def _route(ops, oracle, ids, local_start, local):
 # the LDS ring; decode-sized batches (all skinny), mixed ones and large ones (ring, ragged tails)
 # T = 1: eight single-row slots, every tile small, its quarters dealt out over all workgroups
 @pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 4096, 7168), (4, 256, 8, 4096, 7168),
-                                       (300, 8, 2, 512, 1024), (1, 256, 8, 4096, 7168)])
+                                       (300, 8, 2, 512, 1024), (1, 256, 8, 4096, 7168), (64, 8, 2, 512, 1536),
+                                       (3, 8, 2, 512, 3584)])
 def test_fc1_gated_situ(ops, oracle, T, E, k, m, K):
     _check_fc1(ops, oracle, wl.topk_ids(5 + T, T, E, k), E, m, K)
+
+
+# the reference's own op shapes (moe_fc1 m=6144 k=3584, head.json:25459; moe_fc2 m=3584 k=3072, :25683): 224
+# experts, top-16, this rank's 56 (ids 56..111), T = 300 (tools/trtllm-bmm/probe.py:22). K = 3584 runs the
+# skinny tail (K % 1024 == 512) and the ring's odd count of 512-wide k groups; a decode-sized T = 4 too
+@pytest.mark.parametrize("T", [300, 4])
+def test_fc1_k3_shape(ops, oracle, T):
+    _check_fc1(ops, oracle, wl.topk_ids(70 + T, T, 224, 16), 224, 6144, 3584, local_start=56, local=56)
+
+
+@pytest.mark.parametrize("T", [300, 4])
+def test_fc2_k3_shape(ops, oracle, T):
+    _check_fc2(ops, oracle, wl.topk_ids(71 + T, T, 224, 16), 224, 3584, 3072, local_start=56, local=56)
 
 
 def _split_ids():
@@ -289,15 +304,20 @@ def test_fc2_live_count_is_capped_by_the_tables(ops, oracle):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
-def _check_fc1(ops, oracle, ids, E, m, K):
+def _check_fc1(ops, oracle, ids, E, m, K, local_start=0, local=None):
+    """FC1 through the C ABI over a routed batch, every live slot checked against the oracle (tests/_moe.py)."""
+    from tests import _moe
+
     T = ids.shape[0]
-    ctas, tabs, dev = _route(ops, oracle, ids, 0, E)
+    local = E if local is None else local
+    ctas, tabs, dev = _route(ops, oracle, ids, local_start, local)
     x = wl.activations_bf16(6 + T, T, K)
-    w, sf = wl.mxfp4_weights(8 + T, E, m, K, 119, 124)
+    w, sf = _moe.gpu_raw_weights(ops, torch, 8 + T, local, m, K, 119, 6)
     q, qs = ops.quantize_mxfp8(to_dev(x))
-    wp, sfp = ops.repack_weights(to_dev(w), to_dev(sf), gated=True)
-    alpha = np.full(E, 4.0, np.float32) + np.arange(E, dtype=np.float32) * 0.01
-    beta = np.full(E, 25.0, np.float32)
+    wp, sfp = ops.repack_weights(w, sf, gated=True)
+    del w, sf
+    alpha = np.full(local, 4.0, np.float32) + np.arange(local, dtype=np.float32) * 0.01
+    beta = np.full(local, 25.0, np.float32)
     rows = ctas * 128
     half = m // 2
     c = torch.zeros((rows, half), dtype=torch.uint8, device="cuda")
@@ -307,72 +327,40 @@ def _check_fc1(ops, oracle, ids, E, m, K):
                                         dev["num_non_exiting"], dev["total_padded"], dev["cta_batch"],
                                         dev["cta_limit"], m=m, k=K, ctas=ctas, dbg=dbg)
     _sync()
-    S = int(tabs["num_non_exiting"][0])
-    # check a bounded sample of slots against the oracle (the whole thing at small shapes)
-    slots = list(range(S)) if S <= 16 else list(range(0, S, max(1, S // 12)))[:12]
-    sub = dict(tabs)
-    sub["num_non_exiting"] = np.array([len(slots)], np.int32)
-    sub["cta_batch"] = tabs["cta_batch"][slots]
-    sub["cta_limit"] = (tabs["cta_limit"][slots] - np.array(slots, np.int32) * 128
-                        + np.arange(len(slots), dtype=np.int32) * 128).astype(np.int32)
-    perm = np.concatenate([np.arange(s * 128, s * 128 + 128) for s in slots])
-    sub["route_map"] = tabs["route_map"][perm]
-    ref_c, ref_sfc, ref_dbg = oracle.fc1(to_np(wp), to_np(sfp), to_np(q), to_np(qs), sub, alpha, beta, m, K,
-                                         len(slots) * 128)
-    g = to_np(dbg)[perm]
-    valid = np.concatenate([np.arange(128) < (tabs["cta_limit"][s] - s * 128) for s in slots])
-    assert_gemm_close(g[valid, 0], ref_dbg[valid, 0], "fc1 gate acc")
-    assert_gemm_close(g[valid, 1], ref_dbg[valid, 1], "fc1 up acc")
-    # SiTU-GLU on the kernel's accumulators, against the formula (probe.py:46-47)
-    h_ref = np.vectorize(oracle.situ, otypes=[np.float32])(g[valid, 0], g[valid, 1],
-                                                           alpha[np.repeat(sub["cta_batch"], 128)[valid]][:, None],
-                                                           beta[np.repeat(sub["cta_batch"], 128)[valid]][:, None])
-    np.testing.assert_allclose(g[valid, 2], h_ref, rtol=2e-5, atol=1e-6)
-    # e4m3 codes and ue8m0 scales: bit-exact against the oracle quantiser on the kernel's own h
-    cn = to_np(c)[perm][valid]
-    sfn = to_np(sf_c)
-    qref, sref = oracle.quant_blocks(g[valid, 2])
-    np.testing.assert_array_equal(cn, qref)
-    pv = perm[valid]
-    offs = np.array([[oracle.r128c4_offset(int(p), b, half // 32) for b in range(half // 32)] for p in pv])
-    np.testing.assert_array_equal(sfn[offs], sref)
+    print(f"[fc1] T={T} E={local} m={m} K={K}: {int(tabs['num_non_exiting'][0])} live slots", flush=True)
+    _moe.check_fc1(torch, oracle, wp, sfp, q, qs, tabs, alpha, beta, m, K, c, sf_c, dbg, f"fc1 T={T} K={K}")
 
 
 @pytest.mark.parametrize("T,E,k,m,K", [(64, 8, 2, 512, 1024), (512, 256, 8, 7168, 2048), (4, 256, 8, 7168, 2048),
-                                       (300, 8, 2, 512, 1024), (1, 256, 8, 7168, 2048)])
+                                       (300, 8, 2, 512, 1024), (1, 256, 8, 7168, 2048), (64, 8, 2, 512, 1536),
+                                       (300, 8, 2, 512, 3584), (3, 8, 2, 512, 3584)])
 def test_fc2_bf16(ops, oracle, T, E, k, m, K):
     _check_fc2(ops, oracle, wl.topk_ids(9 + T, T, E, k), E, m, K)
 
 
-def _check_fc2(ops, oracle, ids, E, m, K):
+def _check_fc2(ops, oracle, ids, E, m, K, local_start=0, local=None):
+    """FC2 through the C ABI over a routed batch, every live slot checked against the oracle (tests/_moe.py)."""
+    from tests import _moe
+
     T = ids.shape[0]
-    ctas, tabs, dev = _route(ops, oracle, ids, 0, E)
+    local = E if local is None else local
+    ctas, tabs, dev = _route(ops, oracle, ids, local_start, local)
     rows = ctas * 128
     # activations in permuted row order (what FC1 writes): e4m3 codes and R128c4 scales
     xb = wl.activations_bf16(10 + T, rows, K)
     q_lin, qs_lin = oracle.quant_mxfp8(xb)
     qs_r = np.zeros(oracle.r128c4_size(rows, K // 32), np.uint8)
     qs_r[r128c4_offsets(rows, K // 32)] = qs_lin
-    w, sf = wl.mxfp4_weights(12 + T, E, m, K, 118, 126)
-    wp, sfp = ops.repack_weights(to_dev(w), to_dev(sf))
+    w, sf = _moe.gpu_raw_weights(ops, torch, 12 + T, local, m, K, 118, 9)
+    wp, sfp = ops.repack_weights(w, sf)
+    del w, sf
     c = torch.zeros((rows, m), dtype=torch.bfloat16, device="cuda")
-    ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(wp, sfp, to_dev(q_lin), to_dev(qs_r), c, dev["num_non_exiting"],
-                                      dev["total_padded"], dev["cta_batch"], dev["cta_limit"], m=m, k=K, ctas=ctas,
-                                      sf_b_r128c4=True)
+    qd, qsd = to_dev(q_lin), to_dev(qs_r)
+    ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(wp, sfp, qd, qsd, c, dev["num_non_exiting"], dev["total_padded"],
+                                      dev["cta_batch"], dev["cta_limit"], m=m, k=K, ctas=ctas, sf_b_r128c4=True)
     _sync()
-    S = int(tabs["num_non_exiting"][0])
-    slots = list(range(S)) if S <= 16 else list(range(0, S, max(1, S // 10)))[:10]
-    wpn, sfpn = to_np(wp), to_np(sfp)
-    got = bf16_to_f32(to_np(c))
-    for s in slots:
-        e, lim = int(tabs["cta_batch"][s]), int(tabs["cta_limit"][s])
-        r0 = s * 128
-        sub = {"num_non_exiting": np.array([1], np.int32), "cta_batch": np.array([0], np.int32),
-               "cta_limit": np.array([lim - r0], np.int32)}
-        per_e = m * K // 2
-        _, acc = oracle.fc2(wpn.reshape(-1)[e * per_e:(e + 1) * per_e], sfpn.reshape(-1)[e * per_e // 16:(e + 1) * per_e // 16],
-                            q_lin[r0:r0 + 128], qs_lin[r0:r0 + 128], False, sub, m, K)
-        assert_gemm_close(got[r0:lim], acc[:lim - r0], f"fc2 slot {s}")
+    print(f"[fc2] T={T} E={local} m={m} K={K}: {int(tabs['num_non_exiting'][0])} live slots", flush=True)
+    _moe.check_fc2(torch, oracle, wp, sfp, qd, qsd, tabs, m, K, c, f"fc2 T={T} K={K}")
 
 
 # --------------------------------------------------------------------------------------- MoE glue
