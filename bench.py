@@ -1,6 +1,7 @@
 """Benchmark of the MXFP4 matmul path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemm|decode|moe|stack|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--decode-m 1 4 16]
+                    [--only gemm|decode|moe|stack|mxfp8|k3|peaks|copy]
 
 Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
 
@@ -14,9 +15,9 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
 * Every timed loop is captured once into a HIP graph and replayed, so host launch overhead (Python,
   ctypes, a profiler's API hooks) cannot starve the GPU; back-to-back dispatches then leave no gap, and
   the per-launch averages agree with rocprofv3's per-dispatch durations.
-* `decode` = config 2 at M=1: W4A16 GEMV over [18432, 7168] MXFP4 weights, rotating over enough weight
-  copies (> 256 MB, the Infinity Cache) that every launch streams its weights from HBM; GB/s of
-  algorithmic bytes against the 8 TB/s HBM peak.
+* `decode` = config 2 at M=1 (and M=4, 16 under `more_m`): W4A16 GEMV over [18432, 7168] MXFP4 weights,
+  rotating over enough weight copies (> 256 MB, the Infinity Cache) that every launch streams its weights
+  from HBM; GB/s of algorithmic bytes against the 8 TB/s HBM peak.
 * `moe` = config 4: T=512 tokens, 256 experts, top-8, H=7168, I=2048. One step = moe_quant of the tokens,
   moe_routing, FC1 (gate+up K=7168 -> 2I=4096, SiTU-GLU, MXFP8 out), FC2 (K=2048 -> 7168, bf16 out) and
   moe_finalize_rms (weighted combine of each token's routed rows + RMS norm),
@@ -32,9 +33,17 @@ Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode 
   activations) as GB/s and FLOPs as TFLOP/s.
 * `mxfp8_dense` = extern:cublaslt_mxfp8_tn's analog at config 3's shape with MXFP8 weights: [4096, 7168] x
   [2048, 7168]^T, bf16 out; TFLOP/s against the dense FP8 MFMA peak.
-* `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on a bounded
-  sample of the same GEMM (its first rows), in the headline unit.
-* `traffic` comes from committed rocprofv3 --pmc summaries (profiles/traffic.json), null without one.
+* `k3_fc` = the reference's published hot-path shape: FC1 and FC2 of one EP4 rank's share of K3 prefill at
+  16k tokens (224 experts, top-16, 56 local, H=3584, I=3072, ~65.5k routed rows), ms per layer and TFLOP/s
+  next to GB300's 0.85 / 0.40 ms (docs/roadmap.md:63).
+* `peaks` = measured ceilings on this box (kern_amd/csrc/kern_peaks.hip through the module layer): the
+  scaled MFMA's sustained rate per operand format, the HBM streaming-read rate, one dispatch's cost. The
+  rooflines quote them beside the published peaks (`measured_peak`).
+* `cpu_baseline` = the C oracle (oracle/, scalar C, fp32 accumulation) timed on this host on the same
+  config-3 GEMM, median of 3 runs, one thread per core of the host's CPU share for one GPU (16), with
+  nproc and the CPU model, in the headline unit.
+* `traffic` comes from committed rocprofv3 --pmc summaries (profiles/traffic.json), null without one;
+  `traffic_source` says so.
 
 Inputs are seeded synthetic data (splitmix64, kern_amd/workload.py), generated once before timing.
 """
@@ -65,9 +74,11 @@ def gemv_kernel(M):
 
 # config 4 (MoE grouped)
 MT, ME, MTOP, MH, MI = 512, 256, 8, 7168, 2048
+K3_T = 16384  # K3 prefill tokens of the reference's published FC1 / FC2 timings
 # config 5 (layer stack)
 S_LAYERS, S_QKV, S_OIN, S_MS = 4, 9216, 8192, (1, 64, 2048)
 MALL_BYTES = 256 << 20
+CPU_SHARE = 16  # host cores a one-GPU job may use on these boxes (worker pools are sized to it)
 WARM_MS = 50.0  # untimed graph replays before each timed one
 
 
@@ -77,10 +88,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
-    ap.add_argument("--only", choices=["gemm", "decode", "moe", "stack", "mxfp8", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "decode", "moe", "stack", "mxfp8", "k3", "peaks", "copy"], default=None,
                     help="run one leg only (for profiling); the JSON line then carries that leg. 'copy' runs "
                          "three plain 256 MiB device copies: the reference for scaling HBM byte counters")
-    ap.add_argument("--decode-m", type=int, default=1)
+    ap.add_argument("--decode-m", type=int, nargs="+", default=[1, 4, 16],
+                    help="token counts of the decode leg (the first one is its headline)")
     return ap.parse_args()
 
 
@@ -169,6 +181,10 @@ def step_samples(torch, stream, fn_step, n=50, warmup=5, distinct=8):
             "p90_ms": round(float(np.percentile(t, 90)), 5)}
 
 
+TRAFFIC_SOURCE = "profiles/traffic.json: committed rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled " \
+                 "by a plain copy's counts; read back here, not measured in this run"
+
+
 def load_traffic(kernel):
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -218,11 +234,11 @@ def bench_gemm(torch, ops, wl, stream, steps, warmup):
     }
 
 
-def bench_decode(torch, ops, wl, stream, steps, warmup, M):
+def bench_decode(torch, ops, wl, stream, steps, warmup, Ms):
+    """Config 2 at each M of Ms over the same rotating weight copies."""
     wbytes = DN * DK // 2 + DN * DK // 32
     copies = max(4, -(-2 * MALL_BYTES // wbytes))  # working set > 2x the Infinity Cache
-    log(f"config 2: M={M}, {copies} weight copies of {wbytes / 1e6:.1f} MB")
-    x = dev_from_np(wl.activations_bf16(2, M, DK), torch)
+    log(f"config 2: M={Ms}, {copies} weight copies of {wbytes / 1e6:.1f} MB")
     ws = []
     w_raw = torch.empty((DN, DK // 2), dtype=torch.uint8, device="cuda")
     s_raw = torch.empty((DN, DK // 32), dtype=torch.uint8, device="cuda")
@@ -231,19 +247,93 @@ def bench_decode(torch, ops, wl, stream, steps, warmup, M):
         ops.fill_random_u8(s_raw, wl.tensor_seed(2 + 1000 * j, 4), 122, 11)
         ws.append(ops.repack_weights(w_raw, s_raw))
     del w_raw, s_raw
-    y = torch.empty((M, DN), dtype=torch.bfloat16, device="cuda")
+    res = {}
+    for M in Ms:
+        x = dev_from_np(wl.activations_bf16(2, M, DK), torch)
+        y = torch.empty((M, DN), dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
+
+        def step(i):
+            wp, sp = ws[i % copies]
+            ops.mxfp4_gemv_bf16(x, wp, sp, y, M, N=DN, K=DK)
+
+        log(f"config 2: M={M}: timing {steps} launches after {warmup} warm-up")
+        ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
+        samples = step_samples(torch, stream, step, distinct=copies)
+        nbytes = wbytes + 2 * M * DK + 2 * M * DN
+        res[M] = {"ms_per_step": ms_step, "kernel_ms": ms_step, "bytes": nbytes, "copies": copies,
+                  "samples": samples}
+    return res
+
+
+def bench_k3(torch, ops, wl, stream, steps, warmup):
+    """The reference's published hot-path shape: FC1 and FC2 of one EP4 rank's share of K3 prefill at 16k
+    tokens (docs/roadmap.md:63; picks kernel_index/trtllm_bmm_*.toml): 224 experts, top-16, this rank's 56
+    (ids 56..111), H = 3584, I = 3072 (2I = 6144), T = 16384 tokens routed -> about 65.5k local rows."""
+    T, E, k, L, start, H, I = K3_T, 224, 16, 56, 56, 3584, 3072
+    u8, i32 = torch.uint8, torch.int32
+    log(f"k3: T={T} E={E} top-{k} local {L} H={H} I={I}: generating")
+    ids_np = wl.topk_ids(30, T, E, k)
+    R = int(((ids_np >= start) & (ids_np < start + L)).sum())
+    ids = torch.from_numpy(ids_np).cuda()
+    x = dev_from_np(wl.activations_bf16(31, T, H), torch)
+
+    def weights(seed, rows, K, gated):
+        w_raw = torch.empty((L, rows, K // 2), dtype=u8, device="cuda")
+        s_raw = torch.empty((L, rows, K // 32), dtype=u8, device="cuda")
+        ops.fill_random_u8(w_raw, wl.tensor_seed(seed, 3))
+        ops.fill_random_u8(s_raw, wl.tensor_seed(seed, 4), 119, 6)
+        out = ops.repack_weights(w_raw, s_raw, gated=gated)
+        del w_raw, s_raw
+        return out
+
+    w1, s1 = weights(32, 2 * I, H, True)
+    w2, s2 = weights(33, H, I, False)
+    alpha = torch.full((L,), 4.0, dtype=torch.float32, device="cuda")
+    beta = torch.full((L,), 25.0, dtype=torch.float32, device="cuda")
+    ctas = ops.ctas_bound(T, k, L)
+    rows = ctas * 128
+    tab = {n: torch.zeros(sz, dtype=i32, device="cuda") for n, sz in
+           [("counts", 2 * L), ("cta_batch", ctas), ("cta_limit", ctas), ("nne", 1), ("total_padded", 1),
+            ("route_map", rows), ("exp2perm", T * k)]}
+    q = torch.empty((T, H), dtype=u8, device="cuda")
+    qs = torch.empty((T, H // 32), dtype=u8, device="cuda")
+    c1 = torch.empty((rows, I), dtype=u8, device="cuda")
+    sf1 = torch.empty(ops.r128c4_bytes(rows, I // 32), dtype=u8, device="cuda")
+    c2 = torch.empty((rows, H), dtype=torch.bfloat16, device="cuda")
+    ops.moe_quant(x, q, qs, T, K=H)
+    ops.moe_routing(ids, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"], tab["total_padded"],
+                    tab["route_map"], tab["exp2perm"], tokens=T, topk=k, local_start=start, local_experts=L)
     torch.cuda.synchronize()
+    slots = int(tab["nne"].item())
 
-    def step(i):
-        wp, sp = ws[i % copies]
-        ops.mxfp4_gemv_bf16(x, wp, sp, y, M, N=DN, K=DK)
+    def fc1(i):
+        ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(w1, s1, q, qs, c1, sf1, tab["route_map"], alpha, beta, tab["nne"],
+                                            tab["total_padded"], tab["cta_batch"], tab["cta_limit"], m=2 * I, k=H,
+                                            ctas=ctas)
 
-    log(f"config 2: timing {steps} launches after {warmup} warm-up")
-    ms_step, wall = timed_loop(torch, stream, step, steps, warmup)
-    samples = step_samples(torch, stream, step, distinct=copies)
-    nbytes = wbytes + 2 * M * DK + 2 * M * DN
-    return {"ms_per_step": ms_step, "kernel_ms": ms_step, "bytes": nbytes,
-            "copies": copies, "x": x, "ws": ws, "samples": samples}
+    def fc2(i):
+        ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(w2, s2, c1, sf1, c2, tab["nne"], tab["total_padded"], tab["cta_batch"],
+                                          tab["cta_limit"], m=H, k=I, ctas=ctas, sf_b_r128c4=True)
+
+    n = max(5, min(steps, 40))
+    log(f"k3: {R} local rows in {slots} slots: timing FC1 and FC2, {n} launches each")
+    ms1, _ = timed_loop(torch, stream, fc1, n, min(warmup, 5))
+    ms2, _ = timed_loop(torch, stream, fc2, n, min(warmup, 5))
+    f1 = 2.0 * R * 2 * I * H
+    f2 = 2.0 * R * H * I
+
+    def leg(ms, flop, ref_ms, kernel):
+        t = flop / (ms * 1e-3) / 1e12
+        return {"ms": round(ms, 4), "TFLOP/s": round(t, 1), "frac_fp8_rate": round(t / PEAK_FP8_TFLOPS, 4),
+                "frac_mxfp4_peak": round(t / PEAK_MXFP4_TFLOPS, 4), "algorithmic_flop": flop, "kernel": kernel,
+                "gb300_ms": ref_ms, "vs_gb300": round(ref_ms / ms, 3)}
+
+    return {"metric": "K3 prefill 16k MoE GEMMs, one EP4 rank's share (ms per layer)",
+            "config": {"T": T, "E": E, "topk": k, "local_experts": L, "local_start": start, "H": H, "I": I,
+                       "local_rows": R, "cta_slots": slots, "act": "situ(alpha=4, beta=25)"},
+            "fc1": leg(ms1, f1, 0.85, "kern_mx_bmm_fc1"), "fc2": leg(ms2, f2, 0.40, "kern_mx_bmm_fc2"),
+            "gb300_source": "docs/roadmap.md:63 (trtllm_bmm picks, tile 128)"}
 
 
 def bench_moe(torch, ops, wl, stream, steps, warmup):
@@ -469,23 +559,95 @@ def bench_mxfp8(torch, ops, wl, stream, steps, warmup):
             "config": {"M": M, "N": N, "K": K}}
 
 
+def bench_peaks(torch, ops, stream):
+    """Measured roofline ceilings on this box (kern_amd/csrc/kern_peaks.hip, loaded through the module layer):
+    the scaled MFMA's sustained rate per operand format, the HBM streaming-read rate over a buffer far larger
+    than the Infinity Cache, and the cost of one empty dispatch."""
+    from kern_amd import build as kb
+
+    mod = ops.Module(kb.PEAKS, kb.pinned_sha256("kern_peaks"))
+    src = torch.randint(-2**31, 2**31 - 1, (8192,), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(64, dtype=torch.float32, device="cuda")
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def best_ms(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(reps):
+            ev0.record(stream)
+            fn()
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            t.append(ev0.elapsed_time(ev1))
+        return min(t)
+
+    out = {"source": "kern_amd/csrc/kern_peaks.hip (bench.py --only peaks)"}
+    wgs, steps = 1024, 4096  # 1024 workgroups of 4 waves: 4 waves per SIMD on 256 CUs
+    flop = wgs * 4 * steps * 2.0 * 64 * 64 * 128
+    for shape in ("mfma16", "mfma32"):
+        for fmt in ("fp8_fp8", "fp4_fp8", "fp4_fp4"):
+            e = f"kern_peak_{shape}_{fmt}"
+            ms = best_ms(lambda: mod.launch(e, (wgs,), (256,), src, sink, steps))
+            out[f"{shape}_{fmt}_TFLOPs"] = round(flop / (ms * 1e-3) / 1e12, 1)
+    nbytes = 4 << 30  # 4 GiB: 16x the 256 MB Infinity Cache
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    buf.fill_(3)
+    word = torch.zeros(4, dtype=torch.int32, device="cuda")
+    ms = best_ms(lambda: mod.launch("kern_peak_stream", (256 * 16,), (256,), buf, nbytes // 16, word))
+    out["hbm_read_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    del buf
+    n = 200
+    ev0.record(stream)
+    for _ in range(n):
+        mod.launch("kern_peak_empty", (1,), (64,), word)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    out["empty_dispatch_us"] = round(ev0.elapsed_time(ev1) * 1e3 / n, 2)
+    mod.close()
+    return out
+
+
+def cpu_info():
+    """(nproc, CPU model) of this host, read from os.cpu_count() and /proc/cpuinfo."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return os.cpu_count() or 1, model
+
+
 def cpu_baseline_gemm(torch, wl, tensors):
     """The C oracle on the first rows of the same GEMM (bounded sample), fp32 accumulation."""
     import numpy as np
     from oracle import mxoracle as mo
 
+    import numpy as np
+
     wp, sp, q, qs = tensors
     rows = int(os.environ.get("KERN_BENCH_CPU_ROWS", str(PM)))
-    nt = max(1, min(16, os.cpu_count() or 1))
+    nproc, model = cpu_info()
+    # one thread per core of the host's share for one GPU (16 on these boxes; nproc counts the whole host)
+    nt = max(1, min(CPU_SHARE, nproc))
     wpn, spn = wp.cpu().numpy(), sp.cpu().numpy()
     qn, qsn = q[:rows].cpu().numpy(), qs[:rows].cpu().numpy()
-    t = time.perf_counter()
-    mo.gemm_e4m3_pt(wpn, spn, qn, qsn, PN, PK, 1.0 / 64.0, nthreads=nt)
-    dt = time.perf_counter() - t
+    runs = []
+    for _ in range(3):
+        t = time.perf_counter()
+        mo.gemm_e4m3_pt(wpn, spn, qn, qsn, PN, PK, 1.0 / 64.0, nthreads=nt)
+        runs.append(time.perf_counter() - t)
+    dt = float(np.median(runs))
     flop = 2.0 * rows * PN * PK
     return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": nt, "kind": "port",
-            "sample": f"config 3 GEMM rows 0..{rows - 1} of {PM} (N={PN}, K={PK}), {dt:.1f} s, "
-                      f"scalar C oracle, {nt} threads over rows"}
+            "nproc": nproc, "cpu_model": model, "runs_s": [round(r, 3) for r in runs],
+            "sample": f"config 3 GEMM rows 0..{rows - 1} of {PM} (N={PN}, K={PK}), median of 3 runs "
+                      f"({dt:.2f} s), scalar C oracle (fp32 accumulation), {nt} threads over rows "
+                      f"(the host's CPU share for one GPU; nproc {nproc})"}
 
 
 def main():
@@ -522,7 +684,13 @@ def main():
             g = bench_gemm(torch, ops, wl, stream, args.steps, args.warmup)
         if args.only in (None, "decode"):
             d = bench_decode(torch, ops, wl, stream, args.steps, args.warmup, args.decode_m)
-            d.pop("ws")
+        torch.cuda.synchronize()
+        k3 = pk = None
+        if args.only in (None, "k3"):
+            k3 = bench_k3(torch, ops, wl, stream, args.steps, args.warmup)
+        torch.cuda.synchronize()
+        if args.only in (None, "peaks"):
+            pk = bench_peaks(torch, ops, stream)
         torch.cuda.synchronize()
         if args.only in (None, "moe"):
             mo = bench_moe(torch, ops, wl, stream, args.steps, args.warmup)
@@ -543,24 +711,29 @@ def main():
 
     dec = None
     if d is not None:
-        gbs = d["bytes"] / (d["kernel_ms"] * 1e-3) / 1e9
-        dec = {"metric": f"decode GEMV GB/s M={args.decode_m}", "value": round(gbs, 1), "unit": "GB/s",
-               "ms_per_step": round(d["ms_per_step"], 5),
-               "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                            "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                            "traffic": load_traffic(gemv_kernel(args.decode_m)),
-                            "kernel": gemv_kernel(args.decode_m), "kernel_us": round(d["kernel_ms"] * 1e3, 3),
-
-                            "algorithmic_bytes": d["bytes"]},
-               "samples": d["samples"],
-               "config": {"M": args.decode_m, "N": DN, "K": DK, "weight_copies": d["copies"]}}
+        def dec_leg(M):
+            r = d[M]
+            gbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+            return {"metric": f"decode GEMV GB/s M={M}", "value": round(gbs, 1), "unit": "GB/s",
+                    "ms_per_step": round(r["ms_per_step"], 5),
+                    "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                 "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                 "traffic": load_traffic(gemv_kernel(M)), "traffic_source": TRAFFIC_SOURCE,
+                                 "measured_peak": None if pk is None else pk["hbm_read_GBs"],
+                                 "kernel": gemv_kernel(M), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                                 "algorithmic_bytes": r["bytes"]},
+                    "samples": r["samples"], "config": {"M": M, "N": DN, "K": DK, "weight_copies": r["copies"]}}
+        dec = dec_leg(args.decode_m[0])
+        if len(args.decode_m) > 1:
+            dec["more_m"] = {f"M={M}": dec_leg(M) for M in args.decode_m[1:]}
 
     moe = None
     if mo is not None:
         def hbm(nbytes, ms, kernel):
             gbs = nbytes / (ms * 1e-3) / 1e9
             return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(kernel), "kernel": kernel,
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(kernel),
+                    "traffic_source": TRAFFIC_SOURCE, "kernel": kernel,
                     "kernel_us": round(ms * 1e3, 3), "algorithmic_bytes": nbytes}
         gbs = mo["bytes_step"] / (mo["ms_per_step"] * 1e-3) / 1e9
         moe = {"metric": "MoE grouped step GB/s (config 4)", "value": round(gbs, 1), "unit": "GB/s",
@@ -571,7 +744,10 @@ def main():
                "fc2": hbm(mo["bytes_fc2"], mo["ms_fc2"], "kern_mx_bmm_fc2"),
                "finalize": hbm(mo["bytes_fin"], mo["ms_fin"], "kern_mx_moe_finalize_rms"),
                "config": {"T": MT, "E": ME, "topk": MTOP, "H": MH, "I": MI, "experts_hit": mo["experts_hit"],
-                          "cta_slots": mo["slots"]}}
+                          "cta_slots": mo["slots"],
+                          "act": "situ(alpha=4, beta=25): FC1's fused SiTU-GLU gate, the epilogue of every "
+                                 "reference trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 variant, in place of the config's "
+                                 "separate silu_mul"}}
 
     if g is not None:
         value = g["flop"] / (g["ms_per_step"] * 1e-3) / 1e12
@@ -585,11 +761,12 @@ def main():
                        "M": PM, "N": PN, "K": PK, "step": "moe_quant + mxfp4_gemm_e4m3"},
             "roofline": {"bound": "mfma", "achieved": round(kt, 1), "peak": PEAK_MXFP4_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(kt / PEAK_MXFP4_TFLOPS, 4),
-                         "traffic": load_traffic("kern_mx_gemm_e4m3"),
+                         "traffic": load_traffic("kern_mx_gemm_e4m3"), "traffic_source": TRAFFIC_SOURCE,
                          "kernel": "kern_mx_gemm_e4m3", "kernel_us": round(g["kernel_ms"] * 1e3, 3),
-
                          "algorithmic_flop": g["flop"],
-                         "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4)},
+                         "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4),
+                         "measured_peak": None if pk is None else pk["mfma16_fp4_fp8_TFLOPs"],
+                         "frac_measured_peak": None if pk is None else round(kt / pk["mfma16_fp4_fp8_TFLOPs"], 4)},
             "samples": g["samples"],
             "quantizer": {"kernel": "kern_mx_quant_bf16", "kernel_us": round(g["quant_ms"] * 1e3, 3),
                           "GB/s": round(g["quant_bytes"] / (g["quant_ms"] * 1e-3) / 1e9, 1),
@@ -598,8 +775,16 @@ def main():
             "moe": moe,
             "stack": None if st is None else {"metric": "config 5 layer stack (4 layers, hipGraph)", **st},
             "mxfp8_dense": m8,
+            "k3_fc": k3,
+            "peaks": pk,
             "cpu_baseline": cpu,
         }
+    elif k3 is not None and m8 is None and st is None and dec is None and moe is None:
+        out = dict(k3)
+        out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": False,
+                    "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4xmxfp8->f32", "data": "synthetic"})
+    elif pk is not None and m8 is None and st is None and dec is None and moe is None:
+        out = {"metric": "measured roofline ceilings", **pk, "n_gpus": 1}
     elif m8 is not None and st is None and dec is None and moe is None:
         out = dict(m8)
         out.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,

@@ -137,6 +137,19 @@ int kern_op_plan(const char* op_json, int launch_index, const uint64_t* params, 
                  uint32_t block[3], uint32_t* shared_bytes, void* kernargs, size_t cap, size_t* kernargs_size,
                  int* skip);
 
+/* candidate::splice (crates/kern-manifest/src/candidate.rs:152-185): put a Candidate {modules, ops}
+ * (candidate.rs:34-44; a manifest's `modules` and `ops` sections, each op under the name and with the params
+ * of the op it replaces) into a manifest. Refused with KERN_ERR_MANIFEST, every reason listed ("candidate does
+ * not fit: ..."), when an op is not in the manifest, its params differ from the manifest's, or one of its
+ * launches names a module in neither; otherwise the candidate's modules are taken in (renamed
+ * `<name>@<sha256[0:8]>` where the manifest pins other bytes under the name, candidate.rs:116-131), its ops
+ * replace the manifest's with their launches renamed to match, and modules nothing launches are dropped. The
+ * rest of the manifest is carried over as the same text. Writes the spliced manifest (NUL-terminated) to
+ * out[cap] and its length (without the NUL) to *out_len; out NULL queries the length. The result is then
+ * verified by kern_rt_check / kern_rt_load, as splice ends with verify(). */
+int kern_candidate_splice(const char* manifest_json, const char* candidate_json, char* out, size_t cap,
+                          size_t* out_len);
+
 /* ------------------------------------------------------------------------------------------------
  * Program runtime (kern_amd/csrc/runtime.cpp): a kern manifest's buffers, modules, ops and programs,
  * run by program name with var values, as crates/kern-runtime's Runtime (src/lib.rs:137-236) runs them.
@@ -146,7 +159,9 @@ int kern_op_plan(const char* op_json, int launch_index, const uint64_t* params, 
  * Served manifest subset: vars, buffers of kind input / output / inout / weight / source / workspace /
  * carry on the device, modules by file under kernels_dir pinned by sha256, ops whose launches name one
  * module, programs of one lane with `graph` / `derive`. States, topology, peers, exported or host-placed
- * buffers, extra lanes and checkpoint binding are KERN_ERR_MANIFEST.
+ * buffers and extra lanes are KERN_ERR_MANIFEST. A buffer's checkpoint `bind` and a program's `batch` are
+ * carried, not acted on: weights and sources are the caller's bytes (kern_rt_load_weight), vars the
+ * caller's values.
  * ------------------------------------------------------------------------------------------------ */
 
 typedef struct kern_runtime_s* kern_runtime;
@@ -185,9 +200,19 @@ int kern_rt_capture(kern_runtime rt, const char* program, const char* const* var
                     int nvars);
 int kern_rt_run_captured(kern_runtime rt, const char* program, const char* const* var_names,
                          const uint64_t* var_values, int nvars);
-/* Runtime::time_captured (harness.rs:252-266): mean milliseconds per replay over iters replays. */
+/* Runtime::time_captured (harness.rs:252-266): the median milliseconds of one replay over iters back-to-back
+ * replays, an event between each. */
 int kern_rt_time_captured(kern_runtime rt, const char* program, const char* const* var_names,
                           const uint64_t* var_values, int nvars, int iters, float* ms_per_iter);
+/* Runtime::run_range (harness.rs:186-207): calls [lo, hi) of a (non-derive) program, issued eagerly, then
+ * synchronize. A range outside 0..calls is KERN_ERR_API. */
+int kern_rt_run_range(kern_runtime rt, const char* program, const char* const* var_names, const uint64_t* var_values,
+                      int nvars, int lo, int hi);
+/* Runtime::time_range (harness.rs:209-250): ms_per_call[i] = the GPU milliseconds of call lo + i, issued
+ * eagerly between events, minimum over iters runs of just calls [lo, hi) (a launch gap counts towards the call
+ * after it, as in the reference). ms_per_call holds hi - lo floats. */
+int kern_rt_time_range(kern_runtime rt, const char* program, const char* const* var_names, const uint64_t* var_values,
+                       int nvars, int lo, int hi, int iters, float* ms_per_call);
 int kern_rt_synchronize(kern_runtime rt);
 /* A buffer's device address and bytes (Runtime::buffer_sizes, lib.rs:243). */
 int kern_rt_buffer(kern_runtime rt, const char* name, void** device_ptr, size_t* bytes);

@@ -6,8 +6,8 @@
 2. Its SHA-256 is compiled into libkern_amd.so (the library refuses any other code object) and written
    to kernel_index/kern_mx.toml with the entries and their kernel-argument sizes, the way kern's
    kernel_index pins its modules by digest (tools/kernels/index.py:1-19).
-3. The host side (capi.cpp, manifest_op.cpp, runtime.cpp; no device code) is compiled with g++ against the HIP
-   runtime.
+3. The host side (capi.cpp, manifest_op.cpp, runtime.cpp, candidate.cpp; no device code) is compiled with g++
+   against the HIP runtime.
 """
 from __future__ import annotations
 
@@ -22,6 +22,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HSACO = os.path.join(LIBDIR, "kern_mx.hsaco")
+PEAKS = os.path.join(LIBDIR, "kern_peaks.hsaco")  # roofline probes for bench.py (not on the product path)
 LIB = os.path.join(LIBDIR, "libkern_amd.so")
 ARCH = "gfx950"
 
@@ -95,13 +96,32 @@ def build_code_object(csrc: str = CSRC, out: str = HSACO) -> str:
         return hashlib.sha256(f.read()).hexdigest()
 
 
-def pinned_sha256() -> str:
-    """The sha256 kernel_index/kern_mx.toml pins."""
-    with open(os.path.join(ROOT, "kernel_index", "kern_mx.toml")) as f:
+def build_peaks() -> str:
+    """kern_peaks.hip -> kern_peaks.hsaco, pinned in kernel_index/kern_peaks.toml (bench.py loads it through
+    the module layer with that sha256)."""
+    tmp = PEAKS + ".tmp"
+    flags = [f if f != "-cuid=kern_mx" else "-cuid=kern_peaks" for f in DEVICE_FLAGS]
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", "--no-gpu-bundle-output", *flags,
+          os.path.join(CSRC, "kern_peaks.hip"), "-o", tmp])
+    os.replace(tmp, PEAKS)
+    with open(PEAKS, "rb") as f:
+        sha = hashlib.sha256(f.read()).hexdigest()
+    with open(os.path.join(ROOT, "kernel_index", "kern_peaks.toml"), "w") as f:
+        f.write("\n".join([
+            "# gfx950 roofline probes (kern_amd/csrc/kern_peaks.hip) for bench.py's peaks leg, pinned by sha256",
+            "# (written by kern_amd/build.py). Not part of the MXFP4 path.",
+            "[module]", 'name = "kern_peaks"', 'kind = "hsaco"', f'arch = "{ARCH}"',
+            'source = "kern_amd/lib/kern_peaks.hsaco"', f'sha256 = "{sha}"', ""]))
+    return sha
+
+
+def pinned_sha256(name: str = "kern_mx") -> str:
+    """The sha256 kernel_index/<name>.toml pins."""
+    with open(os.path.join(ROOT, "kernel_index", f"{name}.toml")) as f:
         for line in f:
             if line.startswith("sha256 = "):
                 return line.split('"')[1]
-    raise RuntimeError("kernel_index/kern_mx.toml has no sha256")
+    raise RuntimeError(f"kernel_index/{name}.toml has no sha256")
 
 
 def build_library(sha: str) -> None:
@@ -109,7 +129,7 @@ def build_library(sha: str) -> None:
     _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DKERN_MX_SHA256="{sha}"',
           os.path.join(CSRC, "capi.cpp"), os.path.join(CSRC, "manifest_op.cpp"), os.path.join(CSRC, "runtime.cpp"),
-          "-o", tmp, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+          os.path.join(CSRC, "candidate.cpp"), "-o", tmp, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
           "-ldl"])
     os.replace(tmp, LIB)
 
@@ -135,6 +155,19 @@ def write_index(sha: str) -> None:
         f.write("\n".join(lines))
 
 
+def write_candidate(sha: str) -> None:
+    """kernel_index/k3_moe_candidate.json: the Candidate file of the path's ops at K3's shapes (manifest.py),
+    pinned to this build's code object."""
+    sys.path.insert(0, ROOT)
+    import json
+
+    from kern_amd import manifest
+
+    with open(os.path.join(ROOT, "kernel_index", "k3_moe_candidate.json"), "w") as f:
+        json.dump(manifest.k3_moe_candidate(sha), f, indent=1)
+        f.write("\n")
+
+
 def build_oracle() -> None:
     _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
 
@@ -143,6 +176,8 @@ def build(oracle: bool = True) -> str:
     sha = build_code_object()
     build_library(sha)
     write_index(sha)
+    write_candidate(sha)
+    build_peaks()
     if oracle:
         build_oracle()
     return sha

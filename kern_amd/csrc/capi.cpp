@@ -28,7 +28,7 @@ namespace {
 thread_local std::string g_err;
 
 int fail(int code, const char* fmt, ...) {
-  char buf[1024];
+  char buf[4096];
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(buf, sizeof buf, fmt, ap);
@@ -51,7 +51,7 @@ int hip_fail(hipError_t e, const char* what) {
 
 // the same thread-local message, for the other host source files of the library
 int kern_amd_fail(int code, const char* fmt, ...) {
-  char buf[1024];
+  char buf[4096];
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(buf, sizeof buf, fmt, ap);

@@ -750,13 +750,38 @@ KERN_DEV void tile_of(int gx, int& nx, int& slot) {
   nx = lin % gx;
   slot = lin / gx;
 }
-// MoE tile index lin -> (weight tile nx of gx, slot): slot s belongs to XCD s % 8 (lin % 8), its gx weight
-// tiles back to back, so that the live slots (a prefix) spread evenly over the XCDs and a slot's
-// activation tile is shared within one L2. A bijection on lin >= 0; the slot grows with lin in steps of 8.
-KERN_DEV void moe_tile(int lin, int gx, int& nx, int& slot) {
-  const int j = lin >> 3;
-  nx = j % gx;
-  slot = (j / gx) * 8 + (lin & 7);
+// MoE tile i of workgroup `owner` -> (weight tile nx of gx, slot) among the S live slots. The workgroup
+// runs on XCD x = owner % 8 (the hardware deals workgroups to the XCDs round robin; G is a multiple of 8),
+// as CU c = owner / 8 of the XCD's G/8. XCD x takes the contiguous slots [S*x/8, S*(x+1)/8), so that the
+// slots of one expert (consecutive in the tables) share one L2 and its weights stream from HBM about once,
+// not once per XCD (dealing slot s to XCD s % 8 spread a prefill expert's ~10 slots over all eight L2s).
+// The XCD's CUs walk its tiles in order li = c + (G/8) i, grouped MOE_BS slots at a time; within a group,
+// MOE_BW weight tiles at a time, slot by slot: the G/8 tiles the XCD runs at once share MOE_BS activation
+// tiles and MOE_BW weight tiles through its L2. False when the workgroup has no tile i (li is past the
+// XCD's tiles, and so is every later i).
+#ifndef MOE_BS
+#define MOE_BS 2
+#endif
+#ifndef MOE_BW
+#define MOE_BW 16
+#endif
+KERN_DEV bool moe_tile(int owner, int i, int S, int gx, int G, int& nx, int& slot) {
+  const int x = owner & 7, per = G >> 3;
+  const int s0 = (S * x) >> 3, ns = ((S * (x + 1)) >> 3) - s0;
+  const int li = (owner >> 3) + per * i;
+  if (li >= ns * gx) return false;
+  const int grp = li / (MOE_BS * gx), t = li - grp * (MOE_BS * gx);
+  const int bs = min(MOE_BS, ns - grp * MOE_BS);  // slots of this group (the last may have fewer)
+  const int full = gx / MOE_BW;                   // whole blocks of MOE_BW weight tiles
+  int nb, r, w;
+  if (t < full * bs * MOE_BW) {
+    nb = t / (bs * MOE_BW), r = t - nb * (bs * MOE_BW), w = MOE_BW;
+  } else {
+    nb = full, r = t - full * bs * MOE_BW, w = gx - full * MOE_BW;
+  }
+  slot = s0 + grp * MOE_BS + r / w;
+  nx = nb * MOE_BW + r % w;
+  return true;
 }
 
 // One 128-row (slot or token block) x 256-row (weights) tile on the LDS ring: valid live rows from row0,
@@ -1134,18 +1159,17 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
 }
 
 // The MoE ops (moe_fc1 / moe_fc2): a persistent grid of one workgroup per CU. Workgroup b owns the 256-row
-// weight tiles lin = b + i * G (i = 0, 1, ..; moe_tile with gx = m/256) of the live slots: those of slots
-// of more than skinny_rows rows run on the LDS ring with all 8 waves. The tiles of small slots run in
+// weight tiles moe_tile(b, i) (i = 0, 1, ..; gx = m/256 weight tiles per slot) of the live slots: those of
+// slots of more than skinny_rows rows run on the LDS ring with all 8 waves. The tiles of small slots run in
 // quarters (64 rows, one wave each, no LDS) that the eight waves take one each. In a launch with at most
 // G/2 live tiles (a decode batch: T = 1 gives 128 FC1 tiles, which whole would leave half the CUs idle),
 // quarter o of a small tile owned by workgroup b' runs on workgroup b' + o*G/4, so that the few tiles
 // spread over every CU; otherwise a small tile's quarters all run on its owner. A pass classifies 128
 // candidate tiles of each owner (b alone, or b, b - G/4, b - G/2, b - 3G/4; one per thread, one
-// cta_limit read each) and compacts them into two LDS lists. The owners
-// are congruent mod 8, so along each owner's candidates the slot only grows: the pass whose last
-// candidate of the smallest owner lies past the live slots is the last. Both kinds of work share one
-// launch, so a batch that mixes small and large slots has one tail, and slots past num_non_exiting cost
-// nothing.
+// cta_limit read each) and compacts them into two LDS lists. The owners are congruent mod 8 (one XCD), and
+// an owner's tile i exists only while i is below its share of the XCD's tiles: the pass whose last
+// candidate of the smallest owner has none is the last. Both kinds of work share one launch, so a batch
+// that mixes small and large slots has one tail, and slots past num_non_exiting cost nothing.
 template <int MODE>
 KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1175,8 +1199,8 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
     asm volatile("" : "+v"(tp));
     const int o = tp >> 7, j = tp & 127;
     int nx, slot;
-    moe_tile(owner(o) + G * (base + j), gx, nx, slot);
-    const int v = slot < nne ? A.cta_limit[slot] - slot * BT : 0;
+    const bool any = moe_tile(owner(o), base + j, nne, gx, G, nx, slot);
+    const int v = any ? A.cta_limit[slot] - slot * BT : 0;
     const bool ring = o == 0 && v > kSkinny, skin = v > 0 && v <= kSkinny;
     __syncthreads();  // the previous pass's work is done with the lists and the LDS
     const unsigned long long br = __ballot(ring), bs = __ballot(skin);
@@ -1201,19 +1225,19 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
       if (skin) list[512 + 4 * r + o] = (base + j) * 4 + o;
       ns = 4 * (wcnt[8] + wcnt[9]);
     }
-    // the pass's last candidate of the smallest owner lies past the live slots: no later pass has work
-    moe_tile(bmin + G * (base + 127), gx, nx, slot);
-    const bool last = slot >= nne;
+    // the pass's last candidate of the smallest owner (the first CU of the XCD among the owners) lies past
+    // the XCD's tiles: no later pass has work for any owner
+    const bool last = !moe_tile(bmin, base + 127, nne, gx, G, nx, slot);
     __syncthreads();
     for (int e = 0; e < nr; ++e) {
-      moe_tile(owner(0) + G * list[e], gx, nx, slot);
+      moe_tile(owner(0), list[e], nne, gx, G, nx, slot);
       const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
       if (e) __syncthreads();  // every wave's LDS reads and landing loads of the previous tile are done
       bmm_ring_tile<MODE>(A, L, nx, expert, row0, valid);
     }
     for (int e = wave; e < ns; e += 8) {
       const int code = list[512 + e], q = code & 3;
-      moe_tile(owner(q) + G * (code >> 2), gx, nx, slot);
+      moe_tile(owner(q), code >> 2, nne, gx, G, nx, slot);
       const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
       if (kSkinny <= 16 || valid <= 16)
         skinny_tile<MODE, 1>(A, nx, expert, row0, valid, q, lane);

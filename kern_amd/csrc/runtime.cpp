@@ -12,10 +12,15 @@
 //
 // The manifest subset this runtime serves is the one this path needs: no states, topology, peers or
 // host-placed weights, one lane per program, and `weight` / `source` buffers filled by name from the
-// caller's bytes (kern_rt_load_weight) rather than bound from a checkpoint file. Everything else in the
-// manifest grammar is rejected with KERN_ERR_MANIFEST naming what was found, not ignored.
+// caller's bytes (kern_rt_load_weight). Two fields are carried without being acted on: a buffer's `bind`
+// (the checkpoint tensors the reference's weights loader reads it from, load.rs:336-381; here the caller
+// hands over those bytes) and a program's `batch` (the axes the serving batcher fills, which a caller of
+// kern_rt_run states as var values). Everything else outside the subset is rejected with
+// KERN_ERR_MANIFEST naming what was found, not ignored.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -417,13 +422,17 @@ int dense_vars(const kern_runtime_s& rt, const char* const* names, const uint64_
 }
 
 // issue a program's calls onto the runtime's stream, launch by launch
-int issue_calls(kern_runtime_s& rt, const RtProgram& pg, const std::vector<uint64_t>& dense) {
+// Issue calls [lo, hi) of a program on the runtime's stream; with `after`, event after[ci - lo] is recorded
+// behind call ci (time_range's per-call brackets).
+int issue_calls(kern_runtime_s& rt, const RtProgram& pg, const std::vector<uint64_t>& dense, size_t lo = 0,
+                size_t hi = SIZE_MAX, hipEvent_t* after = nullptr) {
   std::vector<const char*> vn;
   std::vector<uint64_t> vv;
   for (size_t i = 0; i < dense.size(); ++i)
     if (dense[i] != UINT64_MAX) vn.push_back(rt.var_names[i].c_str()), vv.push_back(dense[i]);
   std::vector<uint64_t> params;
-  for (size_t ci = 0; ci < pg.calls.size(); ++ci) {
+  hi = std::min(hi, pg.calls.size());
+  for (size_t ci = lo; ci < hi; ++ci) {
     const RtCall& c = pg.calls[ci];
     const RtOp& op = rt.ops[c.op];
     params.assign(c.args.size(), 0);
@@ -451,9 +460,26 @@ int issue_calls(kern_runtime_s& rt, const RtProgram& pg, const std::vector<uint6
     if (kern_op_launch(op.op, params.data(), (int)params.size(), vn.data(), vv.data(), (int)vn.size(), rt.stream))
       return kern_amd_fail(KERN_ERR_CALL, "program `%s` call #%zu (%s, op `%s`): %s", pg.name.c_str(), ci,
                            c.label.c_str(), op.name.c_str(), kern_last_error());
+    if (after) RT_HIP(hipEventRecord(after[ci - lo], rt.stream), "hipEventRecord");
   }
   return KERN_OK;
 }
+
+// hipEvents released on every path out of a timing call
+struct Events {
+  std::vector<hipEvent_t> ev;
+  ~Events() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  }
+  int create(size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+      hipEvent_t e = nullptr;
+      RT_HIP(hipEventCreate(&e), "hipEventCreate");
+      ev.push_back(e);
+    }
+    return KERN_OK;
+  }
+};
 
 int find_program(kern_runtime_s& rt, const char* name, const RtProgram** out) {
   auto it = rt.prog_index.find(name ? name : "");
@@ -699,22 +725,67 @@ extern "C" int kern_rt_time_captured(kern_runtime rt, const char* program, const
   if (int rc = dense_vars(*rt, var_names, var_values, nvars, dense)) return rc;
   hipGraphExec_t exec = nullptr;
   if (int rc = graph_of(*rt, *pg, dense, &exec)) return rc;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  RT_HIP(hipEventCreate(&e0), "hipEventCreate");
-  if (hipEventCreate(&e1) != hipSuccess) {
-    (void)hipEventDestroy(e0);
-    return kern_amd_fail(KERN_ERR_HIP, "hipEventCreate failed");
+  // back-to-back replays with an event between each, median replay (harness.rs:252-266)
+  Events ev;
+  if (int rc = ev.create((size_t)iters + 1)) return rc;
+  RT_HIP(hipEventRecord(ev.ev[0], rt->stream), "hipEventRecord");
+  for (int i = 0; i < iters; ++i) {
+    RT_HIP(hipGraphLaunch(exec, rt->stream), "hipGraphLaunch");
+    RT_HIP(hipEventRecord(ev.ev[i + 1], rt->stream), "hipEventRecord");
   }
-  hipError_t e = hipEventRecord(e0, rt->stream);
-  for (int i = 0; i < iters && e == hipSuccess; ++i) e = hipGraphLaunch(exec, rt->stream);
-  if (e == hipSuccess) e = hipEventRecord(e1, rt->stream);
-  if (e == hipSuccess) e = hipEventSynchronize(e1);
-  float ms = 0.f;
-  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (e != hipSuccess) return kern_amd_fail(KERN_ERR_HIP, "time_captured: %s", hipGetErrorString(e));
-  *ms_per_iter = ms / (float)iters;
+  RT_HIP(hipEventSynchronize(ev.ev[iters]), "hipEventSynchronize");
+  std::vector<float> t((size_t)iters);
+  for (int i = 0; i < iters; ++i) RT_HIP(hipEventElapsedTime(&t[i], ev.ev[i], ev.ev[i + 1]), "hipEventElapsedTime");
+  std::sort(t.begin(), t.end());
+  *ms_per_iter = t[(size_t)iters / 2];
+  return KERN_OK;
+}
+
+// Runtime::run_range (harness.rs:186-207): calls [lo, hi) of a program, eagerly, then synchronize.
+extern "C" int kern_rt_run_range(kern_runtime rt, const char* program, const char* const* var_names,
+                                 const uint64_t* var_values, int nvars, int lo, int hi) {
+  RT_ENTER(rt);
+  const RtProgram* pg = nullptr;
+  if (int rc = find_program(*rt, program, &pg)) return rc;
+  if (lo < 0 || lo > hi || (size_t)hi > pg->calls.size())
+    return kern_amd_fail(KERN_ERR_API, "program `%s`: call range [%d, %d) outside 0..%zu", pg->name.c_str(), lo, hi,
+                         pg->calls.size());
+  std::vector<uint64_t> dense;
+  if (int rc = dense_vars(*rt, var_names, var_values, nvars, dense)) return rc;
+  if (int rc = issue_calls(*rt, *pg, dense, (size_t)lo, (size_t)hi)) return rc;
+  RT_HIP(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+  return KERN_OK;
+}
+
+// Runtime::time_range (harness.rs:209-250): per-call GPU milliseconds of calls [lo, hi), issued eagerly and
+// bracketed by events, each the minimum over iters runs of just that range; a launch gap counts towards the
+// call after it.
+extern "C" int kern_rt_time_range(kern_runtime rt, const char* program, const char* const* var_names,
+                                  const uint64_t* var_values, int nvars, int lo, int hi, int iters, float* ms_per_call) {
+  RT_ENTER(rt);
+  const RtProgram* pg = nullptr;
+  if (int rc = find_program(*rt, program, &pg)) return rc;
+  if (lo < 0 || lo > hi || (size_t)hi > pg->calls.size())
+    return kern_amd_fail(KERN_ERR_API, "program `%s`: call range [%d, %d) outside 0..%zu", pg->name.c_str(), lo, hi,
+                         pg->calls.size());
+  if (hi > lo && !ms_per_call) return kern_amd_fail(KERN_ERR_API, "time_range: null out pointer");
+  std::vector<uint64_t> dense;
+  if (int rc = dense_vars(*rt, var_names, var_values, nvars, dense)) return rc;
+  const size_t n = (size_t)(hi - lo);
+  Events ev;
+  if (int rc = ev.create(n + 1)) return rc;
+  std::vector<float> best(n, INFINITY);
+  for (int it = 0; it < std::max(iters, 1); ++it) {
+    RT_HIP(hipEventRecord(ev.ev[0], rt->stream), "hipEventRecord");
+    if (int rc = issue_calls(*rt, *pg, dense, (size_t)lo, (size_t)hi, ev.ev.data() + 1)) return rc;
+    RT_HIP(hipStreamSynchronize(rt->stream), "hipStreamSynchronize");
+    for (size_t i = 0; i < n; ++i) {
+      float ms = 0.f;
+      RT_HIP(hipEventElapsedTime(&ms, ev.ev[i], ev.ev[i + 1]), "hipEventElapsedTime");
+      best[i] = std::min(best[i], ms);
+    }
+  }
+  for (size_t i = 0; i < n; ++i) ms_per_call[i] = best[i];
   return KERN_OK;
 }
 

@@ -214,6 +214,28 @@ def moe_ops(H: int, I: int, E: int, topk: int, local_start: int = 0) -> dict:
     }
 
 
+# K3's MoE shapes (crates/kern-manifest/tests/fixtures/k3/head.json): hidden (latent) 3584, intermediate 3072,
+# 224 experts on the one rank of its EP1 prefill stage, top-16
+K3_H, K3_I, K3_E, K3_TOPK = 3584, 3072, 224, 16
+
+
+def candidate(ops: dict, sha256: str, source: str = "kern_mx.hsaco") -> dict:
+    """A Candidate {modules, ops} (crates/kern-manifest/src/candidate.rs:34-44): implementations of a manifest's
+    ops, each under the op's name and with its params, and the module they launch (this build's code object,
+    pinned by sha256; `source` is its file name under the runtime's kernels_dir)."""
+    return {"modules": {MODULE: {"source": source, "sha256": sha256}}, "ops": ops}
+
+
+def k3_moe_candidate(sha256: str, source: str = "kern_mx.hsaco") -> dict:
+    """The candidate for one K3 MoE layer: the path's ops (moe_quant, moe_routing, moe_fc1, moe_fc2,
+    moe_finalize_rms, k3_moe_w_shuffle, k3_moe_sf_shuffle) and the `fill_f32` of its load program (SiTU
+    alpha / beta over the 224 experts) at K3's shapes, all on kern_mx. Spliced into a K3 manifest
+    (kern_candidate_splice), every call of the manifest runs on gfx950 unchanged."""
+    ops = moe_ops(K3_H, K3_I, K3_E, K3_TOPK)
+    ops["fill_f32"] = fill_f32(K3_E)
+    return candidate(ops, sha256, source)
+
+
 def moe_layer_manifest(H: int, I: int, E: int, topk: int, max_tokens: int, sha256: str,
                        source: str = "kern_mx.hsaco", eps: float = 1e-6) -> dict:
     """A whole kern manifest (types.rs:69-97) for one MoE layer of the path on kern_mx, run by the program

@@ -99,7 +99,10 @@ _SIGS = {
     "kern_rt_capture": [P, ctypes.c_char_p, P, P, ctypes.c_int],
     "kern_rt_run_captured": [P, ctypes.c_char_p, P, P, ctypes.c_int],
     "kern_rt_time_captured": [P, ctypes.c_char_p, P, P, ctypes.c_int, ctypes.c_int, P],
+    "kern_rt_run_range": [P, ctypes.c_char_p, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int],
+    "kern_rt_time_range": [P, ctypes.c_char_p, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P],
     "kern_rt_synchronize": [P],
+    "kern_candidate_splice": [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_size_t, P],
     "kern_rt_buffer": [P, ctypes.c_char_p, P, P],
 }
 
@@ -556,6 +559,17 @@ class Runtime:
         n, v, k = self._vars(vars)
         check(lib().kern_rt_run_captured(self._h, program.encode(), n, v, k))
 
+    def run_range(self, program: str, lo: int, hi: int, vars: dict | None = None) -> None:
+        n, v, k = self._vars(vars)
+        check(lib().kern_rt_run_range(self._h, program.encode(), n, v, k, lo, hi))
+
+    def time_range(self, program: str, lo: int, hi: int, vars: dict | None = None, iters: int = 5) -> list:
+        """Per-call GPU ms of calls [lo, hi), each the minimum over iters eager runs (harness.rs:209-250)."""
+        n, v, k = self._vars(vars)
+        out = (ctypes.c_float * max(1, hi - lo))()
+        check(lib().kern_rt_time_range(self._h, program.encode(), n, v, k, lo, hi, iters, out))
+        return [float(out[i]) for i in range(hi - lo)]
+
     def time_captured(self, program: str, vars: dict | None = None, iters: int = 10) -> float:
         n, v, k = self._vars(vars)
         ms = ctypes.c_float()
@@ -567,3 +581,72 @@ class Runtime:
         check(lib().kern_rt_buffer(self._h, name.encode(), ctypes.byref(ptr), ctypes.byref(n)))
         return ptr.value or 0, n.value
 
+
+
+def splice(manifest: dict | str, candidate: dict | str) -> dict:
+    """candidate::splice (crates/kern-manifest/src/candidate.rs:152-185) through kern_candidate_splice: the
+    manifest with the candidate's ops and modules in; KernError(KERN_ERR_MANIFEST) lists every misfit."""
+    mt = manifest if isinstance(manifest, str) else json.dumps(manifest)
+    ct = candidate if isinstance(candidate, str) else json.dumps(candidate)
+    n = ctypes.c_size_t()
+    check(lib().kern_candidate_splice(mt.encode(), ct.encode(), None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    check(lib().kern_candidate_splice(mt.encode(), ct.encode(), buf, n.value + 1, ctypes.byref(n)))
+    return json.loads(buf.value.decode())
+
+
+class Module:
+    """A code object loaded through the module layer (kern_module_load: SHA-256 check, then hipModuleLoadData,
+    the analog of crates/kern-runtime/src/cubin.rs:62-109), with its entries launched by kern_launch: the
+    kernel-argument image is laid out at the offsets the code object's own metadata gives
+    (kern_function_param_offsets / _sizes). Arguments: device tensors (8-byte addresses), ints (as the
+    entry's 4- or 8-byte integer) and floats (f32)."""
+
+    def __init__(self, path: str, sha256: str | None = None):
+        with open(path, "rb") as f:
+            self._img = f.read()
+        h = P()
+        check(lib().kern_module_load(self._img, len(self._img), None if sha256 is None else sha256.encode(),
+                                     ctypes.byref(h)))
+        self._h = h
+        self._fns = {}
+
+    def _fn(self, entry: str):
+        if entry not in self._fns:
+            f = P()
+            check(lib().kern_module_function(self._h, entry.encode(), ctypes.byref(f)))
+            sizes, offs, n = (ctypes.c_uint32 * 64)(), (ctypes.c_uint32 * 64)(), ctypes.c_int()
+            check(lib().kern_function_param_sizes(f, sizes, 64, ctypes.byref(n)))
+            check(lib().kern_function_param_offsets(f, offs, 64, ctypes.byref(n)))
+            self._fns[entry] = (f, list(sizes[: n.value]), list(offs[: n.value]))
+        return self._fns[entry]
+
+    def launch(self, entry: str, grid, block, *args, shared: int = 0) -> None:
+        import struct
+
+        f, sizes, offs = self._fn(entry)
+        if len(args) != len(sizes):
+            raise KernError(4, f"{entry}: {len(args)} arguments, the code object declares {len(sizes)}")
+        img = bytearray(max([o + s for o, s in zip(offs, sizes)] + [8]))
+        for a, s, o in zip(args, sizes, offs):
+            if isinstance(a, torch.Tensor):
+                v = struct.pack("<Q", _ptr(a, entry).value)
+            elif isinstance(a, float):
+                v = struct.pack("<f", a)
+            else:
+                v = int(a).to_bytes(s, "little", signed=int(a) < 0)
+            if len(v) != s:
+                raise KernError(4, f"{entry}: argument of {len(v)} bytes where the code object has {s}")
+            img[o: o + s] = v
+        g = (ctypes.c_uint32 * 3)(*(list(grid) + [1, 1])[:3])
+        b = (ctypes.c_uint32 * 3)(*(list(block) + [1, 1])[:3])
+        buf = (ctypes.c_char * len(img)).from_buffer(img)
+        check(lib().kern_launch(f, g, b, shared, _stream(), buf, len(img)))
+
+    def close(self) -> None:
+        for f, _, _ in self._fns.values():
+            lib().kern_function_release(f)
+        self._fns = {}
+        if self._h:
+            lib().kern_module_unload(self._h)
+            self._h = None
