@@ -683,6 +683,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
     const int half = m >> 1;
     const float al = A.alpha[expert], be = A.beta[expert];
+    const float ial = 1.0f / al, ibe = 1.0f / be, albe = al * be;
     // the wave's 64 interleaved gate/up rows give 32 output columns: one MXFP8 block
     const int ncol0 = (nx * BN + wn * 64) >> 1;
     const int blk = ncol0 >> 5;
@@ -696,9 +697,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
         const v4f v = acc[ts][rs];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          const float gg = v[i], uu = v[i + 2];
-          const float sg = 1.0f / (1.0f + __expf(-gg));
-          h[rs][i] = al * tanhf(gg / al) * sg * be * tanhf(uu / be);
+          h[rs][i] = situ_fast(v[i], v[i + 2], ial, ibe, albe);
         }
       }
       const bool ok = t < valid;

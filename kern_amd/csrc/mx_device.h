@@ -139,6 +139,28 @@ KERN_DEV uint32_t mx_code2(float a, float b, uint32_t sc) {
   return e4m3_hw2(__builtin_ldexpf(a, sh), __builtin_ldexpf(b, sh));
 }
 
+// tanh of an f32 within 4e-7 relative: below |x| = 1/16 the odd Taylor polynomial to x^7 (the next term,
+// 62/2835 x^9, is under 2^-37 |x|); above it (1 - e) / (1 + e) with e = exp(-2|x|) and the sign of x, one
+// exponential and one hardware reciprocal (the cancellation in 1 - e costs at most a factor 7.5 on e's
+// error at |x| = 1/16). NaN stays NaN, +-inf gives +-1.
+KERN_DEV float tanh_fast(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float x2 = x * x;
+  const float p = x * __builtin_fmaf(x2, __builtin_fmaf(x2, __builtin_fmaf(x2, -17.0f / 315.0f, 2.0f / 15.0f),
+                                                         -1.0f / 3.0f), 1.0f);
+  const float e = __expf(-2.0f * ax);
+  const float q = __builtin_copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
+  return ax < 0.0625f ? p : q;
+}
+
+// SiTU-GLU (tools/trtllm-bmm/probe.py:23, :46-47) of gate g and up u, alpha * tanh(g / alpha) * sigmoid(g) *
+// beta * tanh(u / beta), given ial = 1/alpha, ibe = 1/beta and albe = alpha * beta (within 4e-6 relative of
+// the formula): one exponential and one reciprocal for the sigmoid, one of each per tanh, no divides
+KERN_DEV float situ_fast(float g, float u, float ial, float ibe, float albe) {
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+  return albe * tanh_fast(g * ial) * sg * tanh_fast(u * ibe);
+}
+
 // f32 value 2^(code-127) (code 0 is the subnormal 2^-127, 255 is NaN)
 KERN_DEV float e8m0_to_f32(uint32_t code) {
   const uint32_t b = code == 0u ? 0x00400000u : (code == 255u ? 0x7fc00000u : code << 23);  // selects, no branches
