@@ -185,13 +185,14 @@ TRAFFIC_SOURCE = "profiles/traffic.json: committed rocprofv3 --pmc FETCH_SIZE / 
                  "by a plain copy's counts; read back here, not measured in this run"
 
 
-def load_traffic(kernel):
+def load_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.json (key "kernel@workload")."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         d = json.load(f)
-    v = d.get(kernel)
+    v = d.get(f"{kernel}@{workload}")
     return None if v is None else v.get("bytes_per_launch")
 
 
@@ -327,6 +328,7 @@ def bench_k3(torch, ops, wl, stream, steps, warmup):
         t = flop / (ms * 1e-3) / 1e12
         return {"ms": round(ms, 4), "TFLOP/s": round(t, 1), "frac_fp8_rate": round(t / PEAK_FP8_TFLOPS, 4),
                 "frac_mxfp4_peak": round(t / PEAK_MXFP4_TFLOPS, 4), "algorithmic_flop": flop, "kernel": kernel,
+                "traffic": load_traffic(kernel, "k3"), "traffic_source": TRAFFIC_SOURCE,
                 "gb300_ms": ref_ms, "vs_gb300": round(ref_ms / ms, 3)}
 
     return {"metric": "K3 prefill 16k MoE GEMMs, one EP4 rank's share (ms per layer)",
@@ -554,7 +556,7 @@ def bench_mxfp8(torch, ops, wl, stream, steps, warmup):
     t = flop / (ms * 1e-3) / 1e12
     return {"metric": "MXFP8 x MXFP8 dense GEMM TFLOP/s", "value": round(t, 1), "unit": "TFLOP/s",
             "roofline": {"bound": "mfma", "achieved": round(t, 1), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(t / PEAK_FP8_TFLOPS, 4), "traffic": load_traffic("kern_mx_gemm_mxfp8"),
+                         "frac": round(t / PEAK_FP8_TFLOPS, 4), "traffic": load_traffic("kern_mx_gemm_mxfp8", "config3-shape"),
                          "kernel": "kern_mx_gemm_mxfp8", "kernel_us": round(ms * 1e3, 3), "algorithmic_flop": flop},
             "config": {"M": M, "N": N, "K": K}}
 
@@ -718,7 +720,7 @@ def main():
                     "ms_per_step": round(r["ms_per_step"], 5),
                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                  "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                 "traffic": load_traffic(gemv_kernel(M)), "traffic_source": TRAFFIC_SOURCE,
+                                 "traffic": load_traffic(gemv_kernel(M), f"config2-M{M}"), "traffic_source": TRAFFIC_SOURCE,
                                  "measured_peak": None if pk is None else pk["hbm_read_GBs"],
                                  "kernel": gemv_kernel(M), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
                                  "algorithmic_bytes": r["bytes"]},
@@ -732,7 +734,7 @@ def main():
         def hbm(nbytes, ms, kernel):
             gbs = nbytes / (ms * 1e-3) / 1e9
             return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(kernel),
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(kernel, "config4"),
                     "traffic_source": TRAFFIC_SOURCE, "kernel": kernel,
                     "kernel_us": round(ms * 1e3, 3), "algorithmic_bytes": nbytes}
         gbs = mo["bytes_step"] / (mo["ms_per_step"] * 1e-3) / 1e9
@@ -761,7 +763,7 @@ def main():
                        "M": PM, "N": PN, "K": PK, "step": "moe_quant + mxfp4_gemm_e4m3"},
             "roofline": {"bound": "mfma", "achieved": round(kt, 1), "peak": PEAK_MXFP4_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(kt / PEAK_MXFP4_TFLOPS, 4),
-                         "traffic": load_traffic("kern_mx_gemm_e4m3"), "traffic_source": TRAFFIC_SOURCE,
+                         "traffic": load_traffic("kern_mx_gemm_e4m3", "config3"), "traffic_source": TRAFFIC_SOURCE,
                          "kernel": "kern_mx_gemm_e4m3", "kernel_us": round(g["kernel_ms"] * 1e3, 3),
                          "algorithmic_flop": g["flop"],
                          "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4),
