@@ -599,13 +599,15 @@ def bench_peaks(torch, ops, stream):
     ms = best_ms(lambda: mod.launch("kern_peak_stream", (256 * 16,), (256,), buf, nbytes // 16, word))
     out["hbm_read_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
     del buf
+    # back-to-back empty dispatches replayed from one graph: the device-side cost of a dispatch, without
+    # the host's launch rate (an eager Python loop measures that instead)
     n = 200
-    ev0.record(stream)
-    for _ in range(n):
-        mod.launch("kern_peak_empty", (1,), (64,), word)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    out["empty_dispatch_us"] = round(ev0.elapsed_time(ev1) * 1e3 / n, 2)
+    with ops.Graph() as g:
+        for _ in range(n):
+            mod.launch("kern_peak_empty", (1,), (64,), word)
+    ms = best_ms(g.launch)
+    out["empty_dispatch_us"] = round(ms * 1e3 / n, 2)
+    g.close()
     mod.close()
     return out
 
@@ -628,8 +630,6 @@ def cpu_baseline_gemm(torch, wl, tensors):
     """The C oracle on the first rows of the same GEMM (bounded sample), fp32 accumulation."""
     import numpy as np
     from oracle import mxoracle as mo
-
-    import numpy as np
 
     wp, sp, q, qs = tensors
     rows = int(os.environ.get("KERN_BENCH_CPU_ROWS", str(PM)))
