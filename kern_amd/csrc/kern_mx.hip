@@ -637,45 +637,121 @@ struct BmmLds {
 // The tile's epilogue (every mode): lane (c, g) of accumulator (ts, rs) of wave (wt, wn) holds weight
 // rows nx*BN + wn*64 + 16*rs + 4*g + i for tile row wt*64 + 16*ts + c; rows at or past `valid` are not
 // stored.
-template <int MODE>
+// STAGED (the LDS ring's tiles): each wave first writes its 64 output rows into LDS pieces of the ring that
+// only its own loads fill, then stores them back row by row, 16 bytes a lane, so that each store
+// instruction covers whole row segments (128 B a row for bf16, 64 for e4m3, 32 for FC1's e4m3 half): written
+// straight from the accumulators, every store instruction touches 16 rows with 32 bytes (or fewer) each, and
+// at K3's full 128-row slots those scattered pieces took 3-6 us per tile, as long as a fifth of the k-loop.
+// The ring is idle by then: every wave's operand reads of the tile are done before the last multiplies,
+// and this wave's own loads (the only ones into its pieces) have landed.
+// stg: with STAGED, the ring's four stage arrays this wave's group loads (weights for group 0, activations
+// for group 1).
+template <int MODE, bool STAGED>
 KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int wn, int nx, int row0, int valid,
-                           int expert, int lane) {
+                           int expert, int lane, uint8_t* const* stg = nullptr) {
   const int m = A.m;
   const int c = lane & 15, g = lane >> 4;
   const int wrow0 = nx * BN + wn * 64;  // first weight row of this wave
+  // 1 KiB staging piece j of this wave: group 0 wave wn loads weight fragments wn + 4r of each stage,
+  // group 1 wave wn activation blocks wn + 4r; piece j is block wn + 4(j & 1) of stage j / 2 (the stage
+  // index stays a constant: the ring's stages are separate arrays)
+  auto stage = [&](int st) -> uint8_t* { return stg[st]; };
+  auto piece = [&](int j) -> uint8_t* { return stage(j >> 1) + ((j & 1) * 4 + wn) * 1024; };
   if (MODE == MODE_FC2 || MODE == MODE_DENSE_BF16) {
     uint16_t* C = reinterpret_cast<uint16_t*>(A.c);
+    if (A.dbg) {
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      const int t = wt * 64 + ts * 16 + c;
-      if (t < valid) {
-        const int64_t p = row0 + t;
+      for (int ts = 0; ts < 4; ++ts) {
+        const int t = wt * 64 + ts * 16 + c;
+        if (t < valid) {
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs)
+            *reinterpret_cast<v4f*>(A.dbg + (int64_t)(row0 + t) * m + wrow0 + rs * 16 + g * 4) = acc[ts][rs];
+        }
+      }
+    }
+    if (STAGED) {
+      // piece j holds wave rows 8j .. 8j+7, 128 B each (64 bf16), 16-byte unit k of row r at ((k ^ r) << 4)
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts) {
+        const int rr = c & 7;
+        uint8_t* pc = stage(ts) + ((c >> 3) * 4 + wn) * 1024;  // piece 2ts + (c >> 3)
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs) {
-          const int n = wrow0 + rs * 16 + g * 4;
           const v4f v = acc[ts][rs];
-          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
-          uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-          uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-          *reinterpret_cast<uint2*>(C + p * m + n) = make_uint2(lo, hi);
+          const int k = 2 * rs + (g >> 1);
+          *reinterpret_cast<uint2*>(pc + rr * 128 + ((k ^ rr) << 4) + 8 * (g & 1)) =
+              make_uint2(bf16x2_hw(v[0], v[1]), bf16x2_hw(v[2], v[3]));
+        }
+      }
+      const int rr = lane >> 3, k = lane & 7;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const v4u d = *reinterpret_cast<const v4u*>(piece(j) + rr * 128 + ((k ^ rr) << 4));
+        const int t = wt * 64 + 8 * j + rr;
+        if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 8 * k) = d;
+      }
+    } else {
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts) {
+        const int t = wt * 64 + ts * 16 + c;
+        if (t < valid) {
+          const int64_t p = row0 + t;
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs) {
+            const int n = wrow0 + rs * 16 + g * 4;
+            const v4f v = acc[ts][rs];
+            *reinterpret_cast<uint2*>(C + p * m + n) = make_uint2(bf16x2_hw(v[0], v[1]), bf16x2_hw(v[2], v[3]));
+          }
         }
       }
     }
   } else if (MODE == MODE_PT) {
     uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
     const float ds = A.d_scale[0];
+    if (A.dbg) {
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts) {
-      const int t = wt * 64 + ts * 16 + c;
-      if (t < valid) {
-        const int64_t p = row0 + t;
+      for (int ts = 0; ts < 4; ++ts) {
+        const int t = wt * 64 + ts * 16 + c;
+        if (t < valid) {
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs)
+            *reinterpret_cast<v4f*>(A.dbg + (int64_t)(row0 + t) * m + wrow0 + rs * 16 + g * 4) = acc[ts][rs];
+        }
+      }
+    }
+    if (STAGED) {
+      // piece j holds wave rows 16j .. 16j+15, 64 B each (64 e4m3), 16-byte unit k of row r at ((k ^ (r & 3)) << 4)
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts) {
+        uint8_t* pc = piece(ts);
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs) {
-          const int n = wrow0 + rs * 16 + g * 4;
           const v4f v = acc[ts][rs];
-          if (A.dbg) *reinterpret_cast<v4f*>(A.dbg + p * m + n) = v;
-          const uint32_t o = e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
-          *reinterpret_cast<uint32_t*>(C + p * m + n) = o;
+          *reinterpret_cast<uint32_t*>(pc + c * 64 + ((rs ^ (c & 3)) << 4) + 4 * g) =
+              e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
+        }
+      }
+      const int rr = lane >> 2, k = lane & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4u d = *reinterpret_cast<const v4u*>(piece(j) + rr * 64 + ((k ^ (rr & 3)) << 4));
+        const int t = wt * 64 + 16 * j + rr;
+        if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 16 * k) = d;
+      }
+    } else {
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts) {
+        const int t = wt * 64 + ts * 16 + c;
+        if (t < valid) {
+          const int64_t p = row0 + t;
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs) {
+            const int n = wrow0 + rs * 16 + g * 4;
+            const v4f v = acc[ts][rs];
+            const uint32_t o = e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
+            *reinterpret_cast<uint32_t*>(C + p * m + n) = o;
+          }
         }
       }
     }
@@ -721,18 +797,32 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
       amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
       const uint32_t sc = mx_scale_code(amax);
-      if (ok) {
+      if (STAGED) {
+        // piece ts/2 holds wave rows 32(ts/2) .. +31, 32 B each (the wave's MXFP8 block of the row)
+        uint8_t* pc = piece(ts >> 1) + (16 * (ts & 1) + c) * 32 + 2 * g;
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs) *reinterpret_cast<uint16_t*>(pc + 8 * rs) = (uint16_t)mx_code2(h[rs][0], h[rs][1], sc);
+      } else if (ok) {
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs) {
           const int n = ncol0 + 8 * rs + 2 * g;
           const uint32_t o = mx_code2(h[rs][0], h[rs][1], sc);
           *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
         }
-        if (g == 0) {
-          const int64_t kb4 = ((half >> 5) + 3) >> 2;
-          const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
-          A.sf_c[off] = (uint8_t)sc;
-        }
+      }
+      if (ok && g == 0) {
+        const int64_t kb4 = ((half >> 5) + 3) >> 2;
+        const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
+        A.sf_c[off] = (uint8_t)sc;
+      }
+    }
+    if (STAGED) {
+      const int rr = lane >> 1, k = lane & 1;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v4u d = *reinterpret_cast<const v4u*>(piece(j) + rr * 32 + 16 * k);
+        const int t = wt * 64 + 32 * j + rr;
+        if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * half + ncol0 + 16 * k) = d;
       }
     }
   }
@@ -1040,7 +1130,12 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
   // the ring's last requests (clamped re-reads) must land before the workgroup's LDS is released
   WAIT_VMCNT(0);
 
-  bmm_epilogue<MODE>(A, acc, wt, wn, nx, row0, valid, expert, lane);
+  // one call per wave group, each with its own stage arrays (a select between them would put the ring's
+  // pointer table in scratch memory)
+  if (wt == 0)
+    bmm_epilogue<MODE, true>(A, acc, 0, wn, nx, row0, valid, expert, lane, L.w);
+  else
+    bmm_epilogue<MODE, true>(A, acc, 1, wn, nx, row0, valid, expert, lane, L.x);
 }
 
 // Dense modes: one tile per workgroup, grid [m/256, ceil(rows/128)].
@@ -1154,7 +1249,7 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
     compute(IC<0>{}); SKB; compute(IC<1>{}); SKB; compute(IC<2>{}); SKB; compute(IC<3>{}); SKB;
   }
 #undef SKB
-  bmm_epilogue<MODE>(A, acc, 0, hw, nx, row0, valid, expert, lane);
+  bmm_epilogue<MODE, false>(A, acc, 0, hw, nx, row0, valid, expert, lane);
 }
 
 // The MoE ops (moe_fc1 / moe_fc2): a persistent grid of one workgroup per CU. Workgroup b owns the 256-row

@@ -10,8 +10,15 @@
 //   kern_peak_stream: reads n16 16-byte words once (non-temporal loads, four in flight per lane, grid
 //     stride) and folds them into one word per lane, stored only when it equals a fixed value.
 //   kern_peak_empty: nothing (the cost of a dispatch).
+//
+// And a check of a hardware conversion the product kernels rely on:
+//   kern_probe_bf16_cvt: for every f32 bit pattern u in [lo, lo + n), the hardware bf16 packing
+//     (bf16x2_hw, V_CVT_PK_BF16_F32) against the software round-to-nearest-even (f32_to_bf16_bits), on u and
+//     on u with its sign flipped; counts the mismatches into out[0] and leaves one mismatching input in out[1].
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "mx_device.h"
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -126,3 +133,18 @@ extern "C" __global__ __launch_bounds__(256) void kern_peak_stream(const v4u* __
 }
 
 extern "C" __global__ void kern_peak_empty(int* out) { (void)out; }
+
+extern "C" __global__ __launch_bounds__(256) void kern_probe_bf16_cvt(uint32_t lo, uint32_t n, uint32_t* out) {
+  uint32_t bad = 0, which = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += stride) {
+    const uint32_t u = lo + (uint32_t)i, v = u ^ 0x80000000u;
+    const uint32_t hw = bf16x2_hw(__uint_as_float(u), __uint_as_float(v));
+    const uint32_t sw = f32_to_bf16_bits(__uint_as_float(u)) | (f32_to_bf16_bits(__uint_as_float(v)) << 16);
+    if (hw != sw) ++bad, which = u;
+  }
+  if (bad) {
+    atomicAdd(out, bad);
+    out[1] = which;
+  }
+}

@@ -278,3 +278,22 @@ def test_mxfp8_gemm_extreme_scales(ops):
     xd, wd = _deq_x(qa, sa), _deq_x(qw, sw)
     _compare_with_nans(bf16_to_f32(to_np(out)).astype(np.float64), xd @ wd.T, np.abs(xd) @ np.abs(wd).T,
                        "mxfp8 gemm")
+
+
+# ------------------------------------------------------------------------------------ bf16 rounding
+
+def test_bf16_hw_packing_exhaustive(ops):
+    """The GEMM epilogues round to bf16 through V_CVT_PK_BF16_F32 (bf16x2_hw in mx_device.h). On every f32 bit
+    pattern (u in [0, 2^31) and u with its sign bit set) it gives the bits of the device's software
+    round-to-nearest-even f32_to_bf16_bits, the rule of the oracle's bf16 rounding (pinned against torch's cast
+    in tests/test_oracle_codecs.py): ties, subnormals, overflow to infinity, NaN payloads. The probe
+    (kern_peaks.hsaco) counts mismatches on the device."""
+    from kern_amd import build as kb
+
+    mod = ops.Module(kb.PEAKS, kb.pinned_sha256("kern_peaks"))
+    out = torch.zeros(4, dtype=torch.int32, device="cuda")
+    mod.launch("kern_probe_bf16_cvt", (4096,), (256,), 0, 1 << 31, out)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    mod.close()
+    assert got[0] == 0, f"{got[0]} mismatches, e.g. f32 bits {int(got[1]) & 0xffffffff:#010x}"
