@@ -282,6 +282,7 @@ def test_mxfp8_gemm_extreme_scales(ops):
 
 # ------------------------------------------------------------------------------------ bf16 rounding
 
+@pytest.mark.gpu
 def test_bf16_hw_packing_exhaustive(ops):
     """The GEMM epilogues round to bf16 through V_CVT_PK_BF16_F32 (bf16x2_hw in mx_device.h). On every f32 bit
     pattern (u in [0, 2^31) and u with its sign bit set) it gives the bits of the device's software
