@@ -632,31 +632,24 @@ struct BmmLds {
   uint8_t* x[4];
   uint8_t* sw[2];
   uint8_t* sx[2];
+  uint8_t* stg;  // 2 KiB per wave, outside the ring: the epilogue's staging
 };
 
 // The tile's epilogue (every mode): lane (c, g) of accumulator (ts, rs) of wave (wt, wn) holds weight
 // rows nx*BN + wn*64 + 16*rs + 4*g + i for tile row wt*64 + 16*ts + c; rows at or past `valid` are not
 // stored.
-// STAGED (the LDS ring's tiles): each wave first writes its 64 output rows into LDS pieces of the ring that
-// only its own loads fill, then stores them back row by row, 16 bytes a lane, so that each store
-// instruction covers whole row segments (128 B a row for bf16, 64 for e4m3, 32 for FC1's e4m3 half): written
-// straight from the accumulators, every store instruction touches 16 rows with 32 bytes (or fewer) each, and
-// at K3's full 128-row slots those scattered pieces took 3-6 us per tile, as long as a fifth of the k-loop.
-// The ring is idle by then: every wave's operand reads of the tile are done before the last multiplies,
-// and this wave's own loads (the only ones into its pieces) have landed.
-// stg: with STAGED, the ring's four stage arrays this wave's group loads (weights for group 0, activations
-// for group 1).
+// STAGED (the LDS ring's tiles): each wave writes its output rows into its own 2 KiB of LDS (`stg`, outside
+// the ring, so that the next tile's first requests can land in the ring meanwhile), then stores them back
+// row by row, 16 bytes a lane, so that each store instruction covers whole row segments (128 B a row for
+// bf16, 64 for e4m3, 32 for FC1's e4m3 half): written straight from the accumulators, every store
+// instruction touches 16 rows with 32 bytes (or fewer) each, and at K3's full 128-row slots those scattered
+// pieces took 3-6 us per tile, as long as a fifth of the k-loop.
 template <int MODE, bool STAGED>
 KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int wn, int nx, int row0, int valid,
-                           int expert, int lane, uint8_t* const* stg = nullptr) {
+                           int expert, int lane, uint8_t* stg = nullptr) {
   const int m = A.m;
   const int c = lane & 15, g = lane >> 4;
   const int wrow0 = nx * BN + wn * 64;  // first weight row of this wave
-  // 1 KiB staging piece j of this wave: group 0 wave wn loads weight fragments wn + 4r of each stage,
-  // group 1 wave wn activation blocks wn + 4r; piece j is block wn + 4(j & 1) of stage j / 2 (the stage
-  // index stays a constant: the ring's stages are separate arrays)
-  auto stage = [&](int st) -> uint8_t* { return stg[st]; };
-  auto piece = [&](int j) -> uint8_t* { return stage(j >> 1) + ((j & 1) * 4 + wn) * 1024; };
   if (MODE == MODE_FC2 || MODE == MODE_DENSE_BF16) {
     uint16_t* C = reinterpret_cast<uint16_t*>(A.c);
     if (A.dbg) {
@@ -671,25 +664,24 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       }
     }
     if (STAGED) {
-      // piece j holds wave rows 8j .. 8j+7, 128 B each (64 bf16), 16-byte unit k of row r at ((k ^ r) << 4)
+      // one 16-row subtile at a time: row r (128 B, 64 bf16) at r * 128, 16-byte unit k at ((k ^ (r & 7)) << 4)
+      const int rr = lane >> 3, k = lane & 7;
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts) {
-        const int rr = c & 7;
-        uint8_t* pc = stage(ts) + ((c >> 3) * 4 + wn) * 1024;  // piece 2ts + (c >> 3)
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs) {
           const v4f v = acc[ts][rs];
-          const int k = 2 * rs + (g >> 1);
-          *reinterpret_cast<uint2*>(pc + rr * 128 + ((k ^ rr) << 4) + 8 * (g & 1)) =
+          const int kw = 2 * rs + (g >> 1);
+          *reinterpret_cast<uint2*>(stg + c * 128 + ((kw ^ (c & 7)) << 4) + 8 * (g & 1)) =
               make_uint2(bf16x2_hw(v[0], v[1]), bf16x2_hw(v[2], v[3]));
         }
-      }
-      const int rr = lane >> 3, k = lane & 7;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const v4u d = *reinterpret_cast<const v4u*>(piece(j) + rr * 128 + ((k ^ rr) << 4));
-        const int t = wt * 64 + 8 * j + rr;
-        if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 8 * k) = d;
+        for (int h = 0; h < 2; ++h) {
+          const int r = 8 * h + rr;
+          const v4u d = *reinterpret_cast<const v4u*>(stg + r * 128 + ((k ^ (r & 7)) << 4));
+          const int t = wt * 64 + 16 * ts + r;
+          if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 8 * k) = d;
+        }
       }
     } else {
 #pragma unroll
@@ -721,23 +713,26 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       }
     }
     if (STAGED) {
-      // piece j holds wave rows 16j .. 16j+15, 64 B each (64 e4m3), 16-byte unit k of row r at ((k ^ (r & 3)) << 4)
-#pragma unroll
-      for (int ts = 0; ts < 4; ++ts) {
-        uint8_t* pc = piece(ts);
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) {
-          const v4f v = acc[ts][rs];
-          *reinterpret_cast<uint32_t*>(pc + c * 64 + ((rs ^ (c & 3)) << 4) + 4 * g) =
-              e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
-        }
-      }
+      // two 16-row subtiles at a time, subtile ts at (ts & 1) * 1024: row r (64 B, 64 e4m3) at r * 64, 16-byte
+      // unit k at ((k ^ (r & 3)) << 4)
       const int rr = lane >> 2, k = lane & 3;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4u d = *reinterpret_cast<const v4u*>(piece(j) + rr * 64 + ((k ^ (rr & 3)) << 4));
-        const int t = wt * 64 + 16 * j + rr;
-        if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 16 * k) = d;
+      for (int q = 0; q < 2; ++q) {
+#pragma unroll
+        for (int ts = 2 * q; ts < 2 * q + 2; ++ts) {
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs) {
+            const v4f v = acc[ts][rs];
+            *reinterpret_cast<uint32_t*>(stg + (ts & 1) * 1024 + c * 64 + ((rs ^ (c & 3)) << 4) + 4 * g) =
+                e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v4u d = *reinterpret_cast<const v4u*>(stg + j * 1024 + rr * 64 + ((k ^ (rr & 3)) << 4));
+          const int t = wt * 64 + 16 * (2 * q + j) + rr;
+          if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 16 * k) = d;
+        }
       }
     } else {
 #pragma unroll
@@ -798,8 +793,8 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
       const uint32_t sc = mx_scale_code(amax);
       if (STAGED) {
-        // piece ts/2 holds wave rows 32(ts/2) .. +31, 32 B each (the wave's MXFP8 block of the row)
-        uint8_t* pc = piece(ts >> 1) + (16 * (ts & 1) + c) * 32 + 2 * g;
+        // wave row r (32 B: the wave's MXFP8 block of the row) at r * 32
+        uint8_t* pc = stg + (16 * ts + c) * 32 + 2 * g;
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs) *reinterpret_cast<uint16_t*>(pc + 8 * rs) = (uint16_t)mx_code2(h[rs][0], h[rs][1], sc);
       } else if (ok) {
@@ -820,7 +815,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       const int rr = lane >> 1, k = lane & 1;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const v4u d = *reinterpret_cast<const v4u*>(piece(j) + rr * 32 + 16 * k);
+        const v4u d = *reinterpret_cast<const v4u*>(stg + (32 * j + rr) * 32 + 16 * k);
         const int t = wt * 64 + 32 * j + rr;
         if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * half + ncol0 + 16 * k) = d;
       }
@@ -873,55 +868,66 @@ KERN_DEV bool moe_tile(int owner, int i, int S, int gx, int G, int& nx, int& slo
   return true;
 }
 
-// One 128-row (slot or token block) x 256-row (weights) tile on the LDS ring: valid live rows from row0,
-// weights of `expert`.
+// One 128-row (slot or token block) x 256-row (weights) tile on the LDS ring, in three parts so that a
+// persistent workgroup can send the next tile's first requests before the current tile's epilogue:
+// ring_tile (the request sources), ring_prologue (the first requests) and ring_kloop (the multiplies).
+// Two wave groups take turns (ping-pong): group 0 (waves 0-3, token rows 0-63) brings in the weight tiles,
+// group 1 (waves 4-7, rows 64-127) the activation tiles; waves w and w+4 share a SIMD. Every k-tile t has two
+// half-steps separated by workgroup barriers: in the first, group 0 multiplies tile t while group 1 requests
+// activations three tiles ahead and reads tile t's operands; in the second, group 1 multiplies tile t while
+// group 0 requests weights four tiles ahead and reads tile t+1's operands. Each SIMD's matrix core thus
+// always has one wave's MFMAs queued while the other wave's loads are in flight.
+// Every wave fills only its own pieces of the ring: group 0 wave gw the weight fragments gw + 4r and their
+// scale rows, group 1 wave gw the activation blocks gw + 4r and scale rows 4h + gw. Each wave's requests land
+// in the order it sends them, so a wave may send a tile's first requests while its requests of the tile
+// before (the clamped re-reads past the last k-tile) are still in flight.
+struct RingTile {
+  const uint8_t* wbase;     // weight fragment 0, k-tile 0 of the tile (uniform)
+  const uint8_t* sbase;     // its scale dwords (uniform)
+  const uint8_t* xsrc[4];   // group 1: activation request r, k-tile 0 (this lane's 16 bytes)
+  const uint8_t* sx_row[2]; // group 1: activation-scale request h, k group 0 (this lane's dword)
+  int nx, expert, row0, valid;
+};
+
+// live 32-row activation blocks of a tile (group 1's requests per k-tile)
+KERN_DEV int ring_nxr(int valid) { return min(4, max(1, (valid + 31) >> 5)); }
+
 template <int MODE>
-KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int expert, int row0, int valid) {
-  // the wave index through readfirstlane: provably uniform, so everything derived from it (the LDS
-  // bases of the direct loads) lives in scalar registers. The thread index goes through an opaque copy so
-  // that the lane-only addresses are derived anew in each tile: in the persistent MoE kernels they were
-  // hoisted out of the tile loop, spilled, and reloaded behind full memory waits in every tile.
+KERN_DEV RingTile ring_tile(const BmmArgs& A, int nx, int expert, int row0, int valid) {
+  // the wave index through readfirstlane (uniform, so the LDS bases of the requests live in scalar
+  // registers); the thread index through an opaque copy, so that the lane-only addresses are derived anew
+  // for each tile (hoisted out of the persistent loop they stayed live across tiles, were spilled, and were
+  // reloaded behind full memory waits in every tile)
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wt = wave >> 2, wn = wave & 3;  // token half, weight quarter
-  const int K = A.k, KT = K >> 7, KG = K >> 9;
-  const int m = A.m;
-
-  // global sources
+  const int lane = tid & 63, gw = __builtin_amdgcn_readfirstlane(tid >> 6) & 3;
+  const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
+  RingTile T;
+  T.nx = nx, T.expert = expert, T.row0 = row0, T.valid = valid;
   const int rg0 = (nx * BN) >> 4;  // first 16-row group of this tile
-  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)rg0 * KT) * 1024;
-  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)rg0 * KG) * 256;
-  // token (activation row) of tile row t; rows past the slot's last valid row read row/token 0
-  // (their accumulators are never stored)
+  T.wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)rg0 * KT) * 1024;
+  T.sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)rg0 * KG) * 256;
+  // token (activation row) of tile row t; rows past the slot's last valid row read row/token 0 (their
+  // accumulators are never stored)
   auto token_of = [&](int t) -> int64_t {
     if (t >= valid) return 0;
     if (MODE == MODE_FC1) return A.route_map[row0 + t];
     return row0 + t;
   };
-  // Two wave groups take turns (ping-pong): group 0 (waves 0-3, token rows 0-63) brings in the weight
-  // tiles, group 1 (waves 4-7, rows 64-127) the activation tiles; waves w and w+4 share a SIMD. Every
-  // k-tile t has two half-steps separated by workgroup barriers: in the first, group 0 multiplies tile t
-  // while group 1 requests activations three tiles ahead and reads tile t's operands; in the second,
-  // group 1 multiplies tile t while group 0 requests weights four tiles ahead and reads tile t+1's
-  // operands. Each SIMD's matrix core thus always has one wave's MFMAs queued while the other wave's
-  // loads are in flight.
-  const int grp = wt, gw = wn;
-  // group 1: activation request r fills LDS rows 32r + 8*gw + lane/8, position lane%8
+  // activation request r fills LDS rows 32r + 8*gw + lane/8, 16-byte position lane%8, holding chunk
+  // (lane%8) ^ ((row/2)%8) of the row (the swizzle of the X stage)
   const int xpos = lane & 7;
-  const uint8_t* xsrc[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = 32 * r + 8 * gw + (lane >> 3);
-    xsrc[r] = A.b + token_of(t) * K + ((xpos ^ ((t >> 1) & 7)) << 4);
+    T.xsrc[r] = A.b + token_of(t) * K + ((xpos ^ ((t >> 1) & 7)) << 4);
   }
-  // group 1: activation scale dwords of a k group, gathered into LDS as [tile row][k-tile of the group] (16
-  // bytes a row): request h of wave gw fills rows 16*(4h + gw) + lane/4, k-tile lane % 4, so that the
-  // multiplying waves read a row's four k-tiles in one 16-byte read per group instead of one byte read
-  // per k-tile (a k-tile's scale dword holds the row's four 32-wide k blocks). sx_step: between k-tiles,
-  // linear [T][K/32] or R128c4 (one 512-byte tile per 128 rows x 4 k blocks)
+  // activation scale dwords of a k group, gathered into LDS as [tile row][k-tile of the group] (16 bytes a
+  // row): request h of wave gw fills rows 16*(4h + gw) + lane/4, k-tile lane % 4, so that the multiplying
+  // waves read a row's four k-tiles in one 16-byte read per group instead of one byte read per k-tile (a
+  // k-tile's scale dword holds the row's four 32-wide k blocks). Between k-tiles: linear [T][K/32] or R128c4
+  // (one 512-byte tile per 128 rows x 4 k blocks)
   const int sx_step = A.sf_b_r128c4 ? 512 : 4;
-  const uint8_t* sx_row[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int64_t srow = token_of(16 * (4 * h + gw) + (lane >> 2));
@@ -932,46 +938,95 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
     } else {
       base = A.sf_b + srow * (K >> 5);
     }
-    sx_row[h] = base + (lane & 3) * sx_step;
+    T.sx_row[h] = base + (lane & 3) * sx_step;
   }
+  (void)KG;
+  return T;
+}
 
-  // requests (indices past the end are clamped to the last tile / group, whose data is then never
-  // multiplied): group 0 issues 4 per weight tile and 4 per weight-scale group, group 1 NXR (at most 4)
-  // per activation tile and NXS (at most 2) per activation-scale group
-  auto dma_w_tile = [&](int kt, uint8_t* sW) {
-    kt = min(kt, KT - 1);
+// Requests (lane: this thread's lane, from the caller's opaque copy of the thread index; indices past the
+// end are clamped to the last tile / group, whose data is then never
+// multiplied). Group 0: weight tile kt (4 requests) and weight-scale group kg (4); group 1: activation tile
+// kt (NXR requests: only the 32-row blocks that hold live rows) and activation-scale group kg (NXS = 1 or 2:
+// the live 64-row halves). LDS rows of blocks not requested keep stale data that no wave reads (a wave reads
+// the rows of its live 16-row subtiles only); a ring of 17-32-row slots (half of config 4's FC1 slots and
+// most of its FC2 ones) thus issues 5 requests per k-tile instead of 8.
+KERN_DEV void ring_req_w(const RingTile& T, int KT, int gw, int lane, int kt, uint8_t* sW) {
+  kt = min(kt, KT - 1);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int f = r * 4 + gw;  // fragment (16-row group) 0..15
-      dma16(wbase + ((int64_t)f * KT + kt) * 1024 + lane * 16, sW + f * 1024);
-    }
-  };
-  auto dma_w_scales = [&](int kg, uint8_t* sSW) {
-    kg = min(kg, KG - 1);
+  for (int r = 0; r < 4; ++r) {
+    const int f = r * 4 + gw;  // fragment (16-row group) 0..15
+    dma16(T.wbase + ((int64_t)f * KT + kt) * 1024 + lane * 16, sW + f * 1024);
+  }
+}
+KERN_DEV void ring_req_ws(const RingTile& T, int KG, int gw, int lane, int kg, uint8_t* sSW) {
+  kg = min(kg, KG - 1);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int f = r * 4 + gw;
-      dma4(sbase + ((int64_t)f * KG + kg) * 256 + lane * 4, sSW + f * 256);
-    }
-  };
-  // group 1 requests only the 32-row blocks of the activation tile that hold live rows (NXR of 4), and the
-  // scale rows of the live 64-row halves (NXS of 2): LDS rows past them keep stale data that no wave reads
-  // (a wave reads the rows of its live 16-row subtiles only). A ring of 17-32-row slots (half of config 4's
-  // FC1 slots and most of its FC2 ones) thus issues 5 requests per k-tile instead of 8.
-  auto dma_x_tile = [&](int kt, uint8_t* sX, auto NXRc) {
-    constexpr int NXR = decltype(NXRc)::value;
-    kt = min(kt, KT - 1);
+  for (int r = 0; r < 4; ++r) {
+    const int f = r * 4 + gw;
+    dma4(T.sbase + ((int64_t)f * KG + kg) * 256 + lane * 4, sSW + f * 256);
+  }
+}
+template <int NXR>
+KERN_DEV void ring_req_x(const RingTile& T, int KT, int gw, int kt, uint8_t* sX) {
+  kt = min(kt, KT - 1);
 #pragma unroll
-    for (int r = 0; r < NXR; ++r) dma16(xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
-  };
-  auto dma_x_scales = [&](int kg, uint8_t* sSX, auto NXRc) {
-    constexpr int NXS = decltype(NXRc)::value > 2 ? 2 : 1;
-    kg = min(kg, KG - 1);
+  for (int r = 0; r < NXR; ++r) dma16(T.xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
+}
+template <int NXR>
+KERN_DEV void ring_req_xs(const RingTile& T, int KG, int gw, int kg, int sx_step, uint8_t* sSX) {
+  constexpr int NXS = NXR > 2 ? 2 : 1;
+  kg = min(kg, KG - 1);
 #pragma unroll
-    for (int h = 0; h < NXS; ++h) dma4(sx_row[h] + (int64_t)(kg * 4) * sx_step, sSX + 256 * (4 * h + gw));
-  };
+  for (int h = 0; h < NXS; ++h) dma4(T.sx_row[h] + (int64_t)(kg * 4) * sx_step, sSX + 256 * (4 * h + gw));
+}
 
-  v4f acc[4][4];
+// The tile's first requests: group 0 the weight scales of k group 0 and weight tiles 0..3, group 1 the
+// activation scales and activation tiles 0..2. Nothing waits here: ring_kloop waits for them. The caller
+// makes sure that no wave still reads the ring (every wave has passed the previous tile's last barrier).
+template <int MODE>
+KERN_DEV void ring_prologue(const BmmArgs& A, const BmmLds& L, const RingTile& T) {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), gw = wave & 3;
+  const int K = A.k, KT = K >> 7, KG = K >> 9;
+  if (wave < 4) {
+    ring_req_ws(T, KG, gw, lane, 0, L.sw[0]);
+    ring_req_w(T, KT, gw, lane, 0, L.w[0]);
+    ring_req_w(T, KT, gw, lane, 1, L.w[1]);
+    ring_req_w(T, KT, gw, lane, 2, L.w[2]);
+    ring_req_w(T, KT, gw, lane, 3, L.w[3]);
+  } else {
+    const int sx_step = A.sf_b_r128c4 ? 512 : 4;
+    auto go = [&](auto NXRc) {
+      constexpr int NXR = decltype(NXRc)::value;
+      ring_req_xs<NXR>(T, KG, gw, 0, sx_step, L.sx[0]);
+      ring_req_x<NXR>(T, KT, gw, 0, L.x[0]);
+      ring_req_x<NXR>(T, KT, gw, 1, L.x[1]);
+      ring_req_x<NXR>(T, KT, gw, 2, L.x[2]);
+    };
+    switch (ring_nxr(T.valid)) {
+      case 1: go(IC<1>{}); break;
+      case 2: go(IC<2>{}); break;
+      case 3: go(IC<3>{}); break;
+      default: go(IC<4>{}); break;
+    }
+  }
+}
+
+// The tile's multiplies, after ring_prologue: acc = this wave's 64 x 64 block of the tile. Ends with every
+// wave past the tile's last barrier (no wave reads the ring after it); the clamped re-reads past the last
+// k-tile may still be in flight.
+template <int MODE>
+KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v4f (&acc)[4][4]) {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wt = wave >> 2, wn = wave & 3;  // token half, weight quarter
+  const int grp = wt, gw = wn;
+  const int K = A.k, KT = K >> 7, KG = K >> 9;
+  const int valid = T.valid;
+  const int sx_step = A.sf_b_r128c4 ? 512 : 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -985,23 +1040,12 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
     constexpr int NTS = decltype(NTSc)::value;  // live token subtiles of this wave (uniform)
     constexpr int NXR = decltype(NXRc)::value;  // live 32-row activation blocks (group 1's requests)
     constexpr int NXS = NXR > 2 ? 2 : 1;        // activation-scale requests per k group
-    // prologue: group 0 requests the weight scales of group 0 and weight tiles 0..3, group 1 the activation
-    // scales and activation tiles 0..2; tile 0 and the scales have landed once the later tiles' requests
-    // alone are outstanding
-    if (grp == 0) {
-      dma_w_scales(0, L.sw[0]);
-      dma_w_tile(0, L.w[0]);
-      dma_w_tile(1, L.w[1]);
-      dma_w_tile(2, L.w[2]);
-      dma_w_tile(3, L.w[3]);
+    // the prologue's tile 0 and scales have landed once only its later tiles' requests (and whatever this
+    // wave sent after them, such as the previous tile's epilogue stores) are outstanding
+    if (grp == 0)
       WAIT_VMCNT(12);
-    } else {
-      dma_x_scales(0, L.sx[0], NXRc);
-      dma_x_tile(0, L.x[0], NXRc);
-      dma_x_tile(1, L.x[1], NXRc);
-      dma_x_tile(2, L.x[2], NXRc);
+    else
       WAIT_VMCNT(2 * NXR);
-    }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     v4i wa[4];         // W operands of the tile in hand
@@ -1057,8 +1101,8 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       __builtin_amdgcn_sched_barrier(0);
       // second half-step: stage kt%4 is read by both groups; refill it with weight tile kt+4 (the next
       // group's weight scales first), then read tile kt+1
-      if (jt == 0) dma_w_scales(kg + 1, L.sw[sb ^ 1]);
-      dma_w_tile(kt + 4, L.w[st]);
+      if (jt == 0) ring_req_ws(T, KG, gw, lane, kg + 1, L.sw[sb ^ 1]);
+      ring_req_w(T, KT, gw, lane, kt + 4, L.w[st]);
       read_tile(L.w[st1], L.x[st1], L.sw[sb1], L.sx[sb1], (jt + 1) & 3, jt == 3);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
@@ -1071,8 +1115,8 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       // first half-step: activation tile kt+3 into stage (kt+3)%4 (the next group's activation scales
       // first when kt+3 starts it), then this tile's operands, complete before the barrier because
       // group 0 refills the stage next
-      if (jt == 1) dma_x_scales(kg + 1, L.sx[sb ^ 1], NXRc);
-      dma_x_tile(kt + 3, L.x[st3], NXRc);
+      if (jt == 1) ring_req_xs<NXR>(T, KG, gw, kg + 1, sx_step, L.sx[sb ^ 1]);
+      ring_req_x<NXR>(T, KT, gw, kt + 3, L.x[st3]);
       read_tile(L.w[st], L.x[st], L.sw[sb], L.sx[sb], jt, jt == 0);
       WAIT_LGKMCNT0;
       // this wave's activations of tile kt+1 have landed once at most tiles kt+2, kt+3 and the scales
@@ -1096,6 +1140,8 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       if (KG & 1) {  // last (even-numbered) group
         step0(pairs, IC<0>{}); step0(pairs, IC<1>{}); step0(pairs, IC<2>{}); step0(pairs, IC<3>{});
       }
+      // the last read_tile (of the clamped tile past the end) completes before the ring is refilled
+      WAIT_LGKMCNT0;
     } else {
       for (int kk = 0; kk < pairs; ++kk) {
         step1(kk, IC<0>{}); step1(kk, IC<1>{}); step1(kk, IC<2>{}); step1(kk, IC<3>{});
@@ -1118,7 +1164,7 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       default: run(IC<0>{}, IC<4>{}); break;
     }
   } else {
-    switch (min(4, max(1, (valid + 31) >> 5)) * 8 + live_ts) {
+    switch (ring_nxr(valid) * 8 + live_ts) {
       case 1 * 8 + 0: run(IC<0>{}, IC<1>{}); break;
       case 2 * 8 + 0: run(IC<0>{}, IC<2>{}); break;
       case 3 * 8 + 1: run(IC<1>{}, IC<3>{}); break;
@@ -1127,15 +1173,16 @@ KERN_DEV void bmm_ring_tile(const BmmArgs& A, const BmmLds& L, int nx, int exper
       default: run(IC<4>{}, IC<4>{}); break;  // 113-128 rows (and any count past a full tile)
     }
   }
-  // the ring's last requests (clamped re-reads) must land before the workgroup's LDS is released
-  WAIT_VMCNT(0);
+}
 
-  // one call per wave group, each with its own stage arrays (a select between them would put the ring's
-  // pointer table in scratch memory)
-  if (wt == 0)
-    bmm_epilogue<MODE, true>(A, acc, 0, wn, nx, row0, valid, expert, lane, L.w);
-  else
-    bmm_epilogue<MODE, true>(A, acc, 1, wn, nx, row0, valid, expert, lane, L.x);
+// The epilogue of a ring tile: each wave group with its own call (wave-uniform branch), staged through the
+// wave's 2 KiB of `stg`.
+template <int MODE>
+KERN_DEV void ring_epilogue(const BmmArgs& A, const RingTile& T, const v4f (&acc)[4][4], uint8_t* stg) {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // lane values derived per tile (see ring_tile)
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  bmm_epilogue<MODE, true>(A, acc, wave >> 2, wave & 3, T.nx, T.row0, T.valid, T.expert, lane, stg + wave * 2048);
 }
 
 // Dense modes: one tile per workgroup, grid [m/256, ceil(rows/128)].
@@ -1145,15 +1192,23 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   tile_of(A.m / BN, nx, blk);
   const int row0 = blk * BT;
   if (row0 >= A.rows) return;
-  bmm_ring_tile<MODE>(A, L, nx, 0, row0, min(A.rows, row0 + BT) - row0);
+  const RingTile T = ring_tile<MODE>(A, nx, 0, row0, min(A.rows, row0 + BT) - row0);
+  ring_prologue<MODE>(A, L, T);
+  v4f acc[4][4];
+  ring_kloop<MODE>(A, L, T, acc);
+  // the ring's last requests (clamped re-reads) land before the workgroup's LDS is released
+  WAIT_VMCNT(0);
+  ring_epilogue<MODE>(A, T, acc, L.stg);
 }
 
-// the LDS ring of one GEMM workgroup: 4 x (16 + 16) KiB tile stages + 2 x (4 + 2) KiB scale slots = 140 KiB
+// the LDS ring of one GEMM workgroup: 4 x (16 + 16) KiB tile stages + 2 x (4 + 2) KiB scale slots = 140 KiB,
+// and 2 KiB per wave for staging the epilogue's stores (16 KiB)
 #define BMM_LDS_DECL(L)                                                                                  \
   __shared__ __attribute__((aligned(1024))) uint8_t w0_[LDS_W], w1_[LDS_W], w2_[LDS_W], w3_[LDS_W];          \
   __shared__ __attribute__((aligned(1024))) uint8_t x0_[LDS_X], x1_[LDS_X], x2_[LDS_X], x3_[LDS_X];          \
   __shared__ __attribute__((aligned(1024))) uint8_t sw0_[LDS_SW], sw1_[LDS_SW], sx0_[LDS_SX], sx1_[LDS_SX]; \
-  BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}}
+  __shared__ __attribute__((aligned(1024))) uint8_t stg_[8 * 2048];                                          \
+  BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}, stg_}
 
 // Skinny slots (at most skinny_rows routed rows, e.g. an expert's share of a decode batch): nothing to
 // share through LDS, so no ring and no barrier. Four waves (one half of the workgroup) take a 256-row weight
@@ -1163,7 +1218,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
 // independently, so one half's start and end overlap the other's streaming.
 template <int MODE, int NTS>
 KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int valid, int hw, int lane) {
-  // lane-only addresses derived anew in each tile (an opaque copy of the lane index), as in bmm_ring_tile
+  // lane-only addresses derived anew in each tile (an opaque copy of the lane index), as in ring_tile
   asm volatile("" : "+v"(lane));
   const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
   const int c = lane & 15, g = lane >> 4;
@@ -1309,28 +1364,43 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
       ns += wcnt[8 + w];
     }
     const unsigned long long below = (1ull << (tp & 63)) - 1ull;
-    if (ring) list[pr + __popcll(br & below)] = base + j;
+    if (ring) list[pr + __popcll(br & below)] = base + j;  // at most 128: o == 0 only
     if (spread) {
-      if (skin) list[512 + ps + __popcll(bs & below)] = (base + j) * 4 + o;
+      if (skin) list[128 + ps + __popcll(bs & below)] = (base + j) * 4 + o;
     } else {
       // all four thread groups classify the same tiles: quarter o of the r-th small tile goes to 4r + o,
       // so that waves 0-3 take one tile's quarters together and waves 4-7 the next one's
       const int r = ((wave & 1) ? wcnt[8 + wave - 1] : 0) + __popcll(bs & below);
-      if (skin) list[512 + 4 * r + o] = (base + j) * 4 + o;
+      if (skin) list[128 + 4 * r + o] = (base + j) * 4 + o;
       ns = 4 * (wcnt[8] + wcnt[9]);
     }
     // the pass's last candidate of the smallest owner (the first CU of the XCD among the owners) lies past
     // the XCD's tiles: no later pass has work for any owner
     const bool last = !moe_tile(bmin, base + 127, nne, gx, G, nx, slot);
     __syncthreads();
-    for (int e = 0; e < nr; ++e) {
-      moe_tile(owner(0), list[e], nne, gx, G, nx, slot);
-      const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
-      if (e) __syncthreads();  // every wave's LDS reads and landing loads of the previous tile are done
-      bmm_ring_tile<MODE>(A, L, nx, expert, row0, valid);
+    // the ring tiles, software-pipelined: tile e+1's first requests go out right after tile e's multiplies
+    // (every wave has passed tile e's last barrier), before tile e's epilogue, so that their latency passes
+    // during it
+    if (nr > 0) {
+      moe_tile(owner(0), list[0], nne, gx, G, nx, slot);
+      RingTile T = ring_tile<MODE>(A, nx, A.cta_batch[slot], slot * BT, A.cta_limit[slot] - slot * BT);
+      ring_prologue<MODE>(A, L, T);
+      for (int e = 0; e < nr; ++e) {
+        v4f acc[4][4];
+        ring_kloop<MODE>(A, L, T, acc);
+        const RingTile cur = T;
+        if (e + 1 < nr) {
+          moe_tile(owner(0), list[e + 1], nne, gx, G, nx, slot);
+          T = ring_tile<MODE>(A, nx, A.cta_batch[slot], slot * BT, A.cta_limit[slot] - slot * BT);
+          ring_prologue<MODE>(A, L, T);
+        } else {
+          WAIT_VMCNT(0);  // the ring's last requests (clamped re-reads) land before the ring is left
+        }
+        ring_epilogue<MODE>(A, cur, acc, L.stg);
+      }
     }
     for (int e = wave; e < ns; e += 8) {
-      const int code = list[512 + e], q = code & 3;
+      const int code = list[128 + e], q = code & 3;
       moe_tile(owner(q), code >> 2, nne, gx, G, nx, slot);
       const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
       if (kSkinny <= 16 || valid <= 16)
@@ -1357,7 +1427,7 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
   (void)total_padded;
-  __shared__ int list[1024], wcnt[16];
+  __shared__ int list[128 + 512], wcnt[16];  // ring tiles, then small-tile quarters
   bmm_moe<MODE_FC2>(A, L, list, wcnt);
 }
 
@@ -1376,7 +1446,7 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = 0; A.dbg = dbg;
   (void)total_padded;
-  __shared__ int list[1024], wcnt[16];
+  __shared__ int list[128 + 512], wcnt[16];  // ring tiles, then small-tile quarters
   bmm_moe<MODE_FC1>(A, L, list, wcnt);
 }
 
