@@ -616,22 +616,28 @@ struct BmmArgs {
 #define LDS_SX (4 * BT * 4)
 
 
-// 16 bytes per lane from global memory straight into LDS at `lds_wave_base + 16 * lane` (wave-uniform base)
+// 16 bytes per lane from global memory straight into LDS at `lds_wave_base + 16 * lane` (wave-uniform base),
+// GLOBAL_LOAD_LDS_DWORDX4 with the LDS address in M0. Written as inline assembly so that the compiler does
+// not track these loads into LDS: every read of the ring waits for them explicitly (WAIT_VMCNT with the
+// count of requests sent since, then a barrier), and the compiler's own alias tracking could not tell the
+// ring's slots apart and added waits for every load in flight. M0 holds nothing else in the kernels that use
+// these (no other instruction there reads it).
 KERN_DEV void dma16(const void* g, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((glob_void_t*)g, (lds_void_t*)lds_wave_base, 16, 0, 0);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
 }
 // 4 bytes per lane, to `lds_wave_base + 4 * lane`
 KERN_DEV void dma4(const void* g, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((glob_void_t*)g, (lds_void_t*)lds_wave_base, 4, 0, 0);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
 }
 
-// The LDS ring. Each stage and scale slot is its own variable, so that the compiler's wait-count
-// analysis can tell a read of one stage from the loads still landing in another.
+// The LDS ring: four tile stages of each operand, two scale slots of each kind.
 struct BmmLds {
   uint8_t* w[4];
   uint8_t* x[4];
-  uint8_t* sw[2];
-  uint8_t* sx[2];
+  uint8_t* sw;   // two weight-scale slots of LDS_SW bytes (one k group each)
+  uint8_t* sx;   // two activation-scale slots of LDS_SX bytes
   uint8_t* stg;  // 2 KiB per wave, outside the ring: the epilogue's staging
 };
 
@@ -868,24 +874,25 @@ KERN_DEV bool moe_tile(int owner, int i, int S, int gx, int G, int& nx, int& slo
   return true;
 }
 
-// One 128-row (slot or token block) x 256-row (weights) tile on the LDS ring, in three parts so that a
-// persistent workgroup can send the next tile's first requests before the current tile's epilogue:
-// ring_tile (the request sources), ring_prologue (the first requests) and ring_kloop (the multiplies).
+// One 128-row (slot or token block) x 256-row (weights) tile on the LDS ring: ring_tile (where its requests
+// read from), ring_prologue (a first tile's first requests) and ring_kloop (the multiplies).
 // Two wave groups take turns (ping-pong): group 0 (waves 0-3, token rows 0-63) brings in the weight tiles,
 // group 1 (waves 4-7, rows 64-127) the activation tiles; waves w and w+4 share a SIMD. Every k-tile t has two
 // half-steps separated by workgroup barriers: in the first, group 0 multiplies tile t while group 1 requests
 // activations three tiles ahead and reads tile t's operands; in the second, group 1 multiplies tile t while
 // group 0 requests weights four tiles ahead and reads tile t+1's operands. Each SIMD's matrix core thus
 // always has one wave's MFMAs queued while the other wave's loads are in flight.
-// Every wave fills only its own pieces of the ring: group 0 wave gw the weight fragments gw + 4r and their
-// scale rows, group 1 wave gw the activation blocks gw + 4r and scale rows 4h + gw. Each wave's requests land
-// in the order it sends them, so a wave may send a tile's first requests while its requests of the tile
-// before (the clamped re-reads past the last k-tile) are still in flight.
+// Chaining: in a persistent workgroup the requests that run past a tile's last k-tile are the next tile's
+// first ones (its k-tiles 0..3 of weights, 0..2 of activations, and the scales of its first k group), sent
+// during the last four k-steps exactly as in the middle of a tile, so that the next tile starts with its
+// first k-tiles landed: no separate first requests, nothing re-read. Every wave fills only its own pieces of
+// the ring (group 0 wave gw the weight fragments gw + 4r and their scale rows, group 1 wave gw the activation
+// blocks gw + 4r and scale rows 4h + gw), and one wave's requests land in the order it sends them.
 struct RingTile {
-  const uint8_t* wbase;     // weight fragment 0, k-tile 0 of the tile (uniform)
-  const uint8_t* sbase;     // its scale dwords (uniform)
-  const uint8_t* xsrc[4];   // group 1: activation request r, k-tile 0 (this lane's 16 bytes)
-  const uint8_t* sx_row[2]; // group 1: activation-scale request h, k group 0 (this lane's dword)
+  const uint8_t* wbase;  // weight fragment 0, k-tile 0 of the tile (uniform)
+  const uint8_t* sbase;  // its scale dwords (uniform)
+  int xtok[4];           // group 1: activation row (token) of request r (this lane's row)
+  int stok[2];           // group 1: activation row of scale request h
   int nx, expert, row0, valid;
 };
 
@@ -894,10 +901,9 @@ KERN_DEV int ring_nxr(int valid) { return min(4, max(1, (valid + 31) >> 5)); }
 
 template <int MODE>
 KERN_DEV RingTile ring_tile(const BmmArgs& A, int nx, int expert, int row0, int valid) {
-  // the wave index through readfirstlane (uniform, so the LDS bases of the requests live in scalar
-  // registers); the thread index through an opaque copy, so that the lane-only addresses are derived anew
-  // for each tile (hoisted out of the persistent loop they stayed live across tiles, were spilled, and were
-  // reloaded behind full memory waits in every tile)
+  // the wave index through readfirstlane (uniform); the thread index through an opaque copy, so that the
+  // lane-only values are derived anew for each tile (hoisted out of the persistent loop they stayed live
+  // across tiles, were spilled, and were reloaded behind full memory waits in every tile)
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63, gw = __builtin_amdgcn_readfirstlane(tid >> 6) & 3;
@@ -909,50 +915,24 @@ KERN_DEV RingTile ring_tile(const BmmArgs& A, int nx, int expert, int row0, int 
   T.sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)rg0 * KG) * 256;
   // token (activation row) of tile row t; rows past the slot's last valid row read row/token 0 (their
   // accumulators are never stored)
-  auto token_of = [&](int t) -> int64_t {
+  auto token_of = [&](int t) -> int {
     if (t >= valid) return 0;
     if (MODE == MODE_FC1) return A.route_map[row0 + t];
     return row0 + t;
   };
-  // activation request r fills LDS rows 32r + 8*gw + lane/8, 16-byte position lane%8, holding chunk
-  // (lane%8) ^ ((row/2)%8) of the row (the swizzle of the X stage)
-  const int xpos = lane & 7;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = 32 * r + 8 * gw + (lane >> 3);
-    T.xsrc[r] = A.b + token_of(t) * K + ((xpos ^ ((t >> 1) & 7)) << 4);
-  }
-  // activation scale dwords of a k group, gathered into LDS as [tile row][k-tile of the group] (16 bytes a
-  // row): request h of wave gw fills rows 16*(4h + gw) + lane/4, k-tile lane % 4, so that the multiplying
-  // waves read a row's four k-tiles in one 16-byte read per group instead of one byte read per k-tile (a
-  // k-tile's scale dword holds the row's four 32-wide k blocks). Between k-tiles: linear [T][K/32] or R128c4
-  // (one 512-byte tile per 128 rows x 4 k blocks)
-  const int sx_step = A.sf_b_r128c4 ? 512 : 4;
+  for (int r = 0; r < 4; ++r) T.xtok[r] = token_of(32 * r + 8 * gw + (lane >> 3));
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int64_t srow = token_of(16 * (4 * h + gw) + (lane >> 2));
-    const uint8_t* base;
-    if (A.sf_b_r128c4) {
-      const int64_t kb4 = K >> 7;  // ceil(kblocks/4) with K % 128 == 0
-      base = A.sf_b + 512 * ((srow >> 7) * kb4) + (srow & 31) * 16 + ((srow & 127) >> 5) * 4;
-    } else {
-      base = A.sf_b + srow * (K >> 5);
-    }
-    T.sx_row[h] = base + (lane & 3) * sx_step;
-  }
-  (void)KG;
+  for (int h = 0; h < 2; ++h) T.stok[h] = token_of(16 * (4 * h + gw) + (lane >> 2));
   return T;
 }
 
-// Requests (lane: this thread's lane, from the caller's opaque copy of the thread index; indices past the
-// end are clamped to the last tile / group, whose data is then never
-// multiplied). Group 0: weight tile kt (4 requests) and weight-scale group kg (4); group 1: activation tile
-// kt (NXR requests: only the 32-row blocks that hold live rows) and activation-scale group kg (NXS = 1 or 2:
-// the live 64-row halves). LDS rows of blocks not requested keep stale data that no wave reads (a wave reads
-// the rows of its live 16-row subtiles only); a ring of 17-32-row slots (half of config 4's FC1 slots and
-// most of its FC2 ones) thus issues 5 requests per k-tile instead of 8.
+// Requests (lane: this thread's lane, from the caller's opaque copy of the thread index).
+// Group 0: weight tile kt (4 requests), weight-scale group kg (4). Group 1: activation tile kt (NXR requests,
+// the 32-row blocks that hold live rows) and activation-scale group kg (NXS: the live 64-row halves); LDS
+// rows of blocks not requested keep stale data that no wave reads (a wave reads the rows of its live 16-row
+// subtiles only), so a ring of 17-32-row slots issues 5 requests per k-tile instead of 8.
 KERN_DEV void ring_req_w(const RingTile& T, int KT, int gw, int lane, int kt, uint8_t* sW) {
-  kt = min(kt, KT - 1);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int f = r * 4 + gw;  // fragment (16-row group) 0..15
@@ -960,30 +940,58 @@ KERN_DEV void ring_req_w(const RingTile& T, int KT, int gw, int lane, int kt, ui
   }
 }
 KERN_DEV void ring_req_ws(const RingTile& T, int KG, int gw, int lane, int kg, uint8_t* sSW) {
-  kg = min(kg, KG - 1);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int f = r * 4 + gw;
     dma4(T.sbase + ((int64_t)f * KG + kg) * 256 + lane * 4, sSW + f * 256);
   }
 }
-template <int NXR>
-KERN_DEV void ring_req_x(const RingTile& T, int KT, int gw, int kt, uint8_t* sX) {
-  kt = min(kt, KT - 1);
+// Activation requests read through per-tile sources: xs[r], this lane's 16 bytes of request r at k-tile 0,
+// and sxs[h], its scale dword of request h at k group 0 (ring_xsrc). Request r fills LDS rows
+// 32r + 8*gw + lane/8, 16-byte position lane%8, with chunk (lane%8) ^ ((row/2)%8) of the row's k-tile (the X
+// stage's swizzle). Scale dwords of a k group are gathered into LDS as [tile row][k-tile of the group] (16
+// bytes a row): request h fills rows 16*(4h + gw) + lane/4, k-tile lane % 4, so that the multiplying waves
+// read a row's four k-tiles in one 16-byte read per group (a k-tile's scale dword holds the row's four
+// 32-wide k blocks). Scale rows: linear [T][K/32], or R128c4 (one 512-byte tile per 128 rows x 4 k blocks).
+struct RingXSrc {
+  const uint8_t* xs[4];
+  const uint8_t* sxs[2];
+};
+KERN_DEV RingXSrc ring_xsrc(const BmmArgs& A, const RingTile& T, int gw, int lane) {
+  RingXSrc S;
+  const int K = A.k;
 #pragma unroll
-  for (int r = 0; r < NXR; ++r) dma16(T.xsrc[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
+  for (int r = 0; r < 4; ++r) {
+    const int t = 32 * r + 8 * gw + (lane >> 3);
+    S.xs[r] = A.b + (int64_t)T.xtok[r] * K + (((lane & 7) ^ ((t >> 1) & 7)) << 4);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t srow = T.stok[h];
+    S.sxs[h] = A.sf_b_r128c4 ? A.sf_b + 512 * ((srow >> 7) * (int64_t)(K >> 7) + (lane & 3)) + (srow & 31) * 16 +
+                                   ((srow & 127) >> 5) * 4
+                             : A.sf_b + srow * (K >> 5) + (lane & 3) * 4;
+  }
+  return S;
 }
 template <int NXR>
-KERN_DEV void ring_req_xs(const RingTile& T, int KG, int gw, int kg, int sx_step, uint8_t* sSX) {
-  constexpr int NXS = NXR > 2 ? 2 : 1;
-  kg = min(kg, KG - 1);
+KERN_DEV void ring_req_x(const RingXSrc& S, int gw, int kt, uint8_t* sX) {
 #pragma unroll
-  for (int h = 0; h < NXS; ++h) dma4(T.sx_row[h] + (int64_t)(kg * 4) * sx_step, sSX + 256 * (4 * h + gw));
+  for (int r = 0; r < NXR; ++r) dma16(S.xs[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
+}
+// k group kg of the scale rows: 4 k-tiles on, 16 bytes (linear) or four 512-byte tiles (R128c4)
+template <int NXR>
+KERN_DEV void ring_req_xs(const BmmArgs& A, const RingXSrc& S, int gw, int kg, uint8_t* sSX) {
+  constexpr int NXS = NXR > 2 ? 2 : 1;
+  const int64_t step = A.sf_b_r128c4 ? 2048 : 16;
+#pragma unroll
+  for (int h = 0; h < NXS; ++h) dma4(S.sxs[h] + kg * step, sSX + 256 * (4 * h + gw));
 }
 
-// The tile's first requests: group 0 the weight scales of k group 0 and weight tiles 0..3, group 1 the
-// activation scales and activation tiles 0..2. Nothing waits here: ring_kloop waits for them. The caller
-// makes sure that no wave still reads the ring (every wave has passed the previous tile's last barrier).
+// A first tile's first requests (a tile no earlier tile chained to): group 0 the weight scales of k group 0
+// and weight tiles 0..3, group 1 the activation scales and activation tiles 0..2, as the last k-steps of a
+// chained tile send them. Nothing waits here: ring_kloop does. Every wave has passed the previous tile's last
+// barrier (or there is none).
 template <int MODE>
 KERN_DEV void ring_prologue(const BmmArgs& A, const BmmLds& L, const RingTile& T) {
   int tid = threadIdx.x;
@@ -991,19 +999,19 @@ KERN_DEV void ring_prologue(const BmmArgs& A, const BmmLds& L, const RingTile& T
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), gw = wave & 3;
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   if (wave < 4) {
-    ring_req_ws(T, KG, gw, lane, 0, L.sw[0]);
+    ring_req_ws(T, KG, gw, lane, 0, L.sw);
     ring_req_w(T, KT, gw, lane, 0, L.w[0]);
     ring_req_w(T, KT, gw, lane, 1, L.w[1]);
     ring_req_w(T, KT, gw, lane, 2, L.w[2]);
     ring_req_w(T, KT, gw, lane, 3, L.w[3]);
   } else {
-    const int sx_step = A.sf_b_r128c4 ? 512 : 4;
+    const RingXSrc S = ring_xsrc(A, T, gw, lane);
     auto go = [&](auto NXRc) {
       constexpr int NXR = decltype(NXRc)::value;
-      ring_req_xs<NXR>(T, KG, gw, 0, sx_step, L.sx[0]);
-      ring_req_x<NXR>(T, KT, gw, 0, L.x[0]);
-      ring_req_x<NXR>(T, KT, gw, 1, L.x[1]);
-      ring_req_x<NXR>(T, KT, gw, 2, L.x[2]);
+      ring_req_xs<NXR>(A, S, gw, 0, L.sx);
+      ring_req_x<NXR>(S, gw, 0, L.x[0]);
+      ring_req_x<NXR>(S, gw, 1, L.x[1]);
+      ring_req_x<NXR>(S, gw, 2, L.x[2]);
     };
     switch (ring_nxr(T.valid)) {
       case 1: go(IC<1>{}); break;
@@ -1014,11 +1022,17 @@ KERN_DEV void ring_prologue(const BmmArgs& A, const BmmLds& L, const RingTile& T
   }
 }
 
-// The tile's multiplies, after ring_prologue: acc = this wave's 64 x 64 block of the tile. Ends with every
-// wave past the tile's last barrier (no wave reads the ring after it); the clamped re-reads past the last
-// k-tile may still be in flight.
+// The tile's multiplies: acc = this wave's 64 x 64 block. The tile's first requests are out (ring_prologue,
+// or the tile before chained to it, sending all four activation blocks and both scale halves). K group g's
+// scales live in slot g % 2. The last four k-steps send Tn's first requests, with Tn's k group 0 scales into
+// slot 0 as well: with an odd number of k groups that is the slot of T's last group, whose scales every wave
+// has read into registers by then (group 0 at the k-step before the group, group 1 at its first). Without
+// `chain` (Tn is T) they re-read T's last k-tile and scale group instead, so that the counts, and the waits,
+// are the same. Ends with every wave past the tile's last barrier (no wave reads the ring after it); the
+// last requests may still be in flight.
 template <int MODE>
-KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v4f (&acc)[4][4]) {
+KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, const RingTile& Tn, bool chain,
+                         v4f (&acc)[4][4]) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1026,7 +1040,6 @@ KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v
   const int grp = wt, gw = wn;
   const int K = A.k, KT = K >> 7, KG = K >> 9;
   const int valid = T.valid;
-  const int sx_step = A.sf_b_r128c4 ? 512 : 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1035,13 +1048,19 @@ KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v
   // number of live 16-row token subtiles for this wave
   const int live_ts = min(4, max(0, (valid - wt * 64 + 15) >> 4));
   const int c = lane & 15, g = lane >> 4;
+  const RingXSrc S = ring_xsrc(A, T, gw, lane);
+  // past T's last k group: Tn's k group 0, or T's last again
+  const int wn_kg = chain ? 0 : KG - 1;
+  // the scale slots of k group kg
+  auto sw_slot = [&](int kg) -> uint8_t* { return L.sw + (kg & 1) * LDS_SW; };
+  auto sx_slot = [&](int kg) -> uint8_t* { return L.sx + (kg & 1) * LDS_SX; };
 
   auto run = [&](auto NTSc, auto NXRc) {
     constexpr int NTS = decltype(NTSc)::value;  // live token subtiles of this wave (uniform)
     constexpr int NXR = decltype(NXRc)::value;  // live 32-row activation blocks (group 1's requests)
     constexpr int NXS = NXR > 2 ? 2 : 1;        // activation-scale requests per k group
-    // the prologue's tile 0 and scales have landed once only its later tiles' requests (and whatever this
-    // wave sent after them, such as the previous tile's epilogue stores) are outstanding
+    // k-tile 0 and the scales of k group 0 have landed once only tiles 1..3 (1..2 for activations) and
+    // whatever this wave sent after them (such as the tile before's epilogue stores) are outstanding
     if (grp == 0)
       WAIT_VMCNT(12);
     else
@@ -1086,42 +1105,62 @@ KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v
         }
       }
     };
-    // k-tile t = 8*kk + J lives in stage J % 4; its group's scales in slot J / 4 (group parity)
-    auto step0 = [&](int kk, auto Jc) {  // group 0
-      constexpr int J = decltype(Jc)::value;
-      constexpr int jt = J & 3, st = J & 3, st1 = (J + 1) & 3, sb = J >> 2, sb1 = ((J + 1) >> 2) & 1;
-      const int kt = kk * 8 + J, kg = kt >> 2;
+    // k-tile kt (= 4 kg + jt) lives in stage jt, its k group's scales in slot kg % 2. LAST: the tile's last
+    // k group, whose requests four (three) k-tiles ahead are past the end.
+    auto step0 = [&](int kt, auto Jc, auto LASTc) {  // group 0
+      constexpr int jt = decltype(Jc)::value;
+      constexpr bool LAST = decltype(LASTc)::value;
+      const int kg = kt >> 2;
       // first half-step: multiply tile kt (operands read in the previous half-step)
       mfmas(IC<jt>{});
       __builtin_amdgcn_sched_barrier(0);
-      // this wave's weights of tile kt+1 have landed once at most tiles kt+2, kt+3 and the scales
-      // requested with them are outstanding
-      WAIT_VMCNT(8 + ((jt == 1 || jt == 2) ? 4 : 0));
+      // this wave's weights of tile kt+1 have landed once only the requests sent after them are
+      // outstanding: tiles kt+2, kt+3 (4 each) and, for jt = 1, 2, the next group's scales (4). At the last
+      // k-tile there is nothing left to read.
+      if (!LAST || jt < 3) WAIT_VMCNT(8 + ((jt == 1 || jt == 2) ? 4 : 0));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      // second half-step: stage kt%4 is read by both groups; refill it with weight tile kt+4 (the next
+      // second half-step: stage jt is read by both groups; refill it with weight tile kt+4 (the next
       // group's weight scales first), then read tile kt+1
-      if (jt == 0) ring_req_ws(T, KG, gw, lane, kg + 1, L.sw[sb ^ 1]);
-      ring_req_w(T, KT, gw, lane, kt + 4, L.w[st]);
-      read_tile(L.w[st1], L.x[st1], L.sw[sb1], L.sx[sb1], (jt + 1) & 3, jt == 3);
+      if (!LAST) {
+        if (jt == 0) ring_req_ws(T, KG, gw, lane, kg + 1, sw_slot(kg + 1));
+        ring_req_w(T, KT, gw, lane, kt + 4, L.w[jt]);
+      } else {
+        if (jt == 0) ring_req_ws(Tn, KG, gw, lane, wn_kg, L.sw);
+        ring_req_w(Tn, KT, gw, lane, chain ? jt : KT - 1, L.w[jt]);
+      }
+      if (!LAST || jt < 3)
+        read_tile(L.w[(jt + 1) & 3], L.x[(jt + 1) & 3], sw_slot((kt + 1) >> 2), sx_slot((kt + 1) >> 2), (jt + 1) & 3,
+                  jt == 3);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     };
-    auto step1 = [&](int kk, auto Jc) {  // group 1
-      constexpr int J = decltype(Jc)::value;
-      constexpr int jt = J & 3, st = J & 3, st3 = (J + 3) & 3, sb = J >> 2;
-      const int kt = kk * 8 + J, kg = kt >> 2;
-      // first half-step: activation tile kt+3 into stage (kt+3)%4 (the next group's activation scales
+    auto step1 = [&](int kt, auto Jc, auto LASTc) {  // group 1
+      constexpr int jt = decltype(Jc)::value;
+      constexpr bool LAST = decltype(LASTc)::value;
+      const int kg = kt >> 2;
+      // first half-step: activation tile kt+3 into stage (jt+3)%4 (the next group's activation scales
       // first when kt+3 starts it), then this tile's operands, complete before the barrier because
-      // group 0 refills the stage next
-      if (jt == 1) ring_req_xs<NXR>(T, KG, gw, kg + 1, sx_step, L.sx[sb ^ 1]);
-      ring_req_x<NXR>(T, KT, gw, kt + 3, L.x[st3]);
-      read_tile(L.w[st], L.x[st], L.sw[sb], L.sx[sb], jt, jt == 0);
+      // group 0 refills the stage next. In the last group, tile kt+3 is past the end from jt = 1 on: Tn's
+      // tile jt-1 with all four blocks and both scale halves (Tn's live rows are not this tile's).
+      if (!LAST || jt == 0) {
+        if (!LAST && jt == 1) ring_req_xs<NXR>(A, S, gw, kg + 1, sx_slot(kg + 1));
+        ring_req_x<NXR>(S, gw, kt + 3, L.x[(jt + 3) & 3]);
+      } else {
+        const RingXSrc Sn = ring_xsrc(A, Tn, gw, lane);
+        if (jt == 1) ring_req_xs<4>(A, Sn, gw, wn_kg, L.sx);
+        ring_req_x<4>(Sn, gw, chain ? jt - 1 : KT - 1, L.x[(jt + 3) & 3]);
+      }
+      read_tile(L.w[jt], L.x[jt], sw_slot(kg), sx_slot(kg), jt, jt == 0);
       WAIT_LGKMCNT0;
-      // this wave's activations of tile kt+1 have landed once at most tiles kt+2, kt+3 and the scales
-      // requested with them are outstanding
-      WAIT_VMCNT(2 * NXR + ((jt == 1 || jt == 2) ? NXS : 0));
+      // this wave's activations of tile kt+1 have landed once only the requests sent after them are
+      // outstanding: tiles kt+2, kt+3 (NXR each) and, for jt = 1, 2, the next group's scales (NXS); in the
+      // last group the requests past the end are 4 blocks and 2 scale halves
+      if (!LAST)
+        WAIT_VMCNT(2 * NXR + ((jt == 1 || jt == 2) ? NXS : 0));
+      else if (jt < 3)
+        WAIT_VMCNT(jt == 0 ? 2 * NXR : (jt == 1 ? NXR + 6 : 10));
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       // second half-step: multiply tile kt
@@ -1130,26 +1169,23 @@ KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     };
-    const int pairs = KG >> 1;
+    // k groups 0 .. KG-2 (no request past the end), then the last one
+    constexpr auto N = IC<0>{};
+    constexpr auto Y = IC<1>{};
+    const int kt_last = KT - 4;
     if (grp == 0) {
-      read_tile(L.w[0], L.x[0], L.sw[0], L.sx[0], 0, true);
-      for (int kk = 0; kk < pairs; ++kk) {
-        step0(kk, IC<0>{}); step0(kk, IC<1>{}); step0(kk, IC<2>{}); step0(kk, IC<3>{});
-        step0(kk, IC<4>{}); step0(kk, IC<5>{}); step0(kk, IC<6>{}); step0(kk, IC<7>{});
+      read_tile(L.w[0], L.x[0], sw_slot(0), sx_slot(0), 0, true);
+      for (int kt = 0; kt < kt_last; kt += 4) {
+        step0(kt, IC<0>{}, N); step0(kt + 1, IC<1>{}, N); step0(kt + 2, IC<2>{}, N); step0(kt + 3, IC<3>{}, N);
       }
-      if (KG & 1) {  // last (even-numbered) group
-        step0(pairs, IC<0>{}); step0(pairs, IC<1>{}); step0(pairs, IC<2>{}); step0(pairs, IC<3>{});
-      }
-      // the last read_tile (of the clamped tile past the end) completes before the ring is refilled
-      WAIT_LGKMCNT0;
+      step0(kt_last, IC<0>{}, Y); step0(kt_last + 1, IC<1>{}, Y);
+      step0(kt_last + 2, IC<2>{}, Y); step0(kt_last + 3, IC<3>{}, Y);
     } else {
-      for (int kk = 0; kk < pairs; ++kk) {
-        step1(kk, IC<0>{}); step1(kk, IC<1>{}); step1(kk, IC<2>{}); step1(kk, IC<3>{});
-        step1(kk, IC<4>{}); step1(kk, IC<5>{}); step1(kk, IC<6>{}); step1(kk, IC<7>{});
+      for (int kt = 0; kt < kt_last; kt += 4) {
+        step1(kt, IC<0>{}, N); step1(kt + 1, IC<1>{}, N); step1(kt + 2, IC<2>{}, N); step1(kt + 3, IC<3>{}, N);
       }
-      if (KG & 1) {
-        step1(pairs, IC<0>{}); step1(pairs, IC<1>{}); step1(pairs, IC<2>{}); step1(pairs, IC<3>{});
-      }
+      step1(kt_last, IC<0>{}, Y); step1(kt_last + 1, IC<1>{}, Y);
+      step1(kt_last + 2, IC<2>{}, Y); step1(kt_last + 3, IC<3>{}, Y);
     }
   };
   // group 0 (weights, token rows 0-63) by its live subtiles; group 1 (activations, rows 64-127) by its live
@@ -1175,8 +1211,7 @@ KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, v
   }
 }
 
-// The epilogue of a ring tile: each wave group with its own call (wave-uniform branch), staged through the
-// wave's 2 KiB of `stg`.
+// The epilogue of a ring tile, staged through the wave's 2 KiB of `stg`.
 template <int MODE>
 KERN_DEV void ring_epilogue(const BmmArgs& A, const RingTile& T, const v4f (&acc)[4][4], uint8_t* stg) {
   int tid = threadIdx.x;
@@ -1195,10 +1230,10 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   const RingTile T = ring_tile<MODE>(A, nx, 0, row0, min(A.rows, row0 + BT) - row0);
   ring_prologue<MODE>(A, L, T);
   v4f acc[4][4];
-  ring_kloop<MODE>(A, L, T, acc);
-  // the ring's last requests (clamped re-reads) land before the workgroup's LDS is released
-  WAIT_VMCNT(0);
+  ring_kloop<MODE>(A, L, T, T, false, acc);
   ring_epilogue<MODE>(A, T, acc, L.stg);
+  // the last (clamped) requests land before the workgroup's LDS is released
+  WAIT_VMCNT(0);
 }
 
 // the LDS ring of one GEMM workgroup: 4 x (16 + 16) KiB tile stages + 2 x (4 + 2) KiB scale slots = 140 KiB,
@@ -1206,9 +1241,9 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
 #define BMM_LDS_DECL(L)                                                                                  \
   __shared__ __attribute__((aligned(1024))) uint8_t w0_[LDS_W], w1_[LDS_W], w2_[LDS_W], w3_[LDS_W];          \
   __shared__ __attribute__((aligned(1024))) uint8_t x0_[LDS_X], x1_[LDS_X], x2_[LDS_X], x3_[LDS_X];          \
-  __shared__ __attribute__((aligned(1024))) uint8_t sw0_[LDS_SW], sw1_[LDS_SW], sx0_[LDS_SX], sx1_[LDS_SX]; \
+  __shared__ __attribute__((aligned(1024))) uint8_t sw_[2 * LDS_SW], sx_[2 * LDS_SX];                      \
   __shared__ __attribute__((aligned(1024))) uint8_t stg_[8 * 2048];                                          \
-  BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, {sw0_, sw1_}, {sx0_, sx1_}, stg_}
+  BmmLds L = {{w0_, w1_, w2_, w3_}, {x0_, x1_, x2_, x3_}, sw_, sx_, stg_}
 
 // Skinny slots (at most skinny_rows routed rows, e.g. an expert's share of a decode batch): nothing to
 // share through LDS, so no ring and no barrier. Four waves (one half of the workgroup) take a 256-row weight
@@ -1320,7 +1355,7 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
 // candidate of the smallest owner has none is the last. Both kinds of work share one launch, so a batch
 // that mixes small and large slots has one tail, and slots past num_non_exiting cost nothing.
 template <int MODE>
-KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
+KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, int* lval, int* wcnt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // the live slots, never more than the tables hold (a corrupt count cannot send reads past them)
   const int nne = min(A.num_non_exiting[0], A.max_slots);
@@ -1350,6 +1385,7 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
     int nx, slot;
     const bool any = moe_tile(owner(o), base + j, nne, gx, G, nx, slot);
     const int v = any ? A.cta_limit[slot] - slot * BT : 0;
+    const int ex = o == 0 && v > kSkinny ? A.cta_batch[slot] : 0;
     const bool ring = o == 0 && v > kSkinny, skin = v > 0 && v <= kSkinny;
     __syncthreads();  // the previous pass's work is done with the lists and the LDS
     const unsigned long long br = __ballot(ring), bs = __ballot(skin);
@@ -1364,7 +1400,12 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
       ns += wcnt[8 + w];
     }
     const unsigned long long below = (1ull << (tp & 63)) - 1ull;
-    if (ring) list[pr + __popcll(br & below)] = base + j;  // at most 128: o == 0 only
+    if (ring) {  // at most 128: o == 0 only
+      const int at = pr + __popcll(br & below);
+      list[at] = base + j;
+      lexp[at] = ex;
+      lval[at] = v;
+    }
     if (spread) {
       if (skin) list[128 + ps + __popcll(bs & below)] = (base + j) * 4 + o;
     } else {
@@ -1378,26 +1419,25 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* wcnt) {
     // the XCD's tiles: no later pass has work for any owner
     const bool last = !moe_tile(bmin, base + 127, nne, gx, G, nx, slot);
     __syncthreads();
-    // the ring tiles, software-pipelined: tile e+1's first requests go out right after tile e's multiplies
-    // (every wave has passed tile e's last barrier), before tile e's epilogue, so that their latency passes
-    // during it
+    // the ring tiles, chained: each tile's last k-steps send the next one's first requests (ring_kloop)
     if (nr > 0) {
       moe_tile(owner(0), list[0], nne, gx, G, nx, slot);
-      RingTile T = ring_tile<MODE>(A, nx, A.cta_batch[slot], slot * BT, A.cta_limit[slot] - slot * BT);
+      RingTile T = ring_tile<MODE>(A, nx, lexp[0], slot * BT, lval[0]);
       ring_prologue<MODE>(A, L, T);
       for (int e = 0; e < nr; ++e) {
-        v4f acc[4][4];
-        ring_kloop<MODE>(A, L, T, acc);
-        const RingTile cur = T;
-        if (e + 1 < nr) {
+        const bool chain = e + 1 < nr;
+        RingTile Tn = T;
+        if (chain) {
           moe_tile(owner(0), list[e + 1], nne, gx, G, nx, slot);
-          T = ring_tile<MODE>(A, nx, A.cta_batch[slot], slot * BT, A.cta_limit[slot] - slot * BT);
-          ring_prologue<MODE>(A, L, T);
-        } else {
-          WAIT_VMCNT(0);  // the ring's last requests (clamped re-reads) land before the ring is left
+          Tn = ring_tile<MODE>(A, nx, lexp[e + 1], slot * BT, lval[e + 1]);
         }
-        ring_epilogue<MODE>(A, cur, acc, L.stg);
+        v4f acc[4][4];
+        ring_kloop<MODE>(A, L, T, Tn, chain, acc);
+        ring_epilogue<MODE>(A, T, acc, L.stg);
+        T = Tn;
       }
+      // the last tile's (clamped) requests land before the ring is used again or the LDS released
+      WAIT_VMCNT(0);
     }
     for (int e = wave; e < ns; e += 8) {
       const int code = list[128 + e], q = code & 3;
@@ -1427,8 +1467,9 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
   (void)total_padded;
-  __shared__ int list[128 + 512], wcnt[16];  // ring tiles, then small-tile quarters
-  bmm_moe<MODE_FC2>(A, L, list, wcnt);
+  // the pass's ring tiles (their expert and live rows beside them), then its small-tile quarters
+  __shared__ int list[128 + 512], lexp[128], lval[128], wcnt[16];
+  bmm_moe<MODE_FC2>(A, L, list, lexp, lval, wcnt);
 }
 
 // op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
@@ -1446,8 +1487,9 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
   A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = 0; A.dbg = dbg;
   (void)total_padded;
-  __shared__ int list[128 + 512], wcnt[16];  // ring tiles, then small-tile quarters
-  bmm_moe<MODE_FC1>(A, L, list, wcnt);
+  // the pass's ring tiles (their expert and live rows beside them), then its small-tile quarters
+  __shared__ int list[128 + 512], lexp[128], lval[128], wcnt[16];
+  bmm_moe<MODE_FC1>(A, L, list, lexp, lval, wcnt);
 }
 
 // Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).
