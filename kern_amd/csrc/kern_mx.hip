@@ -649,7 +649,12 @@ struct BmmLds {
 // row by row, 16 bytes a lane, so that each store instruction covers whole row segments (128 B a row for
 // bf16, 64 for e4m3, 32 for FC1's e4m3 half): written straight from the accumulators, every store
 // instruction touches 16 rows with 32 bytes (or fewer) each, and at K3's full 128-row slots those scattered
-// pieces took 3-6 us per tile, as long as a fifth of the k-loop.
+// pieces took 3-6 us per tile, as long as a fifth of the k-loop. The staged stores are buffer stores whose
+// range ends at the tile's last live row, so that rows past it are dropped by the hardware rather than
+// branched around: every wave sends the same number of stores per tile (epi_stores), and the next tile's
+// first wait can count them.
+template <int MODE>
+constexpr int epi_stores() { return MODE == MODE_FC1 ? 2 + 4 : (MODE == MODE_PT ? 4 : 8); }
 template <int MODE, bool STAGED>
 KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int wn, int nx, int row0, int valid,
                            int expert, int lane, uint8_t* stg = nullptr) {
@@ -672,6 +677,8 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     if (STAGED) {
       // one 16-row subtile at a time: row r (128 B, 64 bf16) at r * 128, 16-byte unit k at ((k ^ (r & 7)) << 4)
       const int rr = lane >> 3, k = lane & 7;
+      const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(C + (int64_t)row0 * m), (short)0, max(valid, 0) * m * 2, 0x00020000);
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts) {
 #pragma unroll
@@ -686,7 +693,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
           const int r = 8 * h + rr;
           const v4u d = *reinterpret_cast<const v4u*>(stg + r * 128 + ((k ^ (r & 7)) << 4));
           const int t = wt * 64 + 16 * ts + r;
-          if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 8 * k) = d;
+          __builtin_amdgcn_raw_buffer_store_b128(d, cr, (t * m + wrow0 + 8 * k) * 2, 0, 0);
         }
       }
     } else {
@@ -722,6 +729,8 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       // two 16-row subtiles at a time, subtile ts at (ts & 1) * 1024: row r (64 B, 64 e4m3) at r * 64, 16-byte
       // unit k at ((k ^ (r & 3)) << 4)
       const int rr = lane >> 2, k = lane & 3;
+      const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(C + (int64_t)row0 * m), (short)0, max(valid, 0) * m, 0x00020000);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
 #pragma unroll
@@ -737,7 +746,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
         for (int j = 0; j < 2; ++j) {
           const v4u d = *reinterpret_cast<const v4u*>(stg + j * 1024 + rr * 64 + ((k ^ (rr & 3)) << 4));
           const int t = wt * 64 + 16 * (2 * q + j) + rr;
-          if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * m + wrow0 + 16 * k) = d;
+          __builtin_amdgcn_raw_buffer_store_b128(d, cr, t * m + wrow0 + 16 * k, 0, 0);
         }
       }
     } else {
@@ -764,6 +773,9 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     // the wave's 64 interleaved gate/up rows give 32 output columns: one MXFP8 block
     const int ncol0 = (nx * BN + wn * 64) >> 1;
     const int blk = ncol0 >> 5;
+    // sf_c: R128c4 over the tables' max_slots * 128 rows
+    const __amdgpu_buffer_rsrc_t sfr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)A.sf_c, (short)0, A.max_slots * ((((half >> 5) + 3) >> 2) * 512), 0x00020000);
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       const int t = wt * 64 + ts * 16 + c;
@@ -811,7 +823,13 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
           *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
         }
       }
-      if (ok && g == 0) {
+      if (STAGED) {
+        // one byte store per subtile from every lane, the lanes other than g = 0 and the rows past the
+        // tile's live ones pointed past the end of sf_c (dropped)
+        const int64_t kb4 = ((half >> 5) + 3) >> 2;
+        const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)sc, sfr, ok && g == 0 ? (int)off : 0x7fffff00, 0, 0);
+      } else if (ok && g == 0) {
         const int64_t kb4 = ((half >> 5) + 3) >> 2;
         const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
         A.sf_c[off] = (uint8_t)sc;
@@ -819,11 +837,13 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     }
     if (STAGED) {
       const int rr = lane >> 1, k = lane & 1;
+      const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(C + (int64_t)row0 * half), (short)0, max(valid, 0) * half, 0x00020000);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const v4u d = *reinterpret_cast<const v4u*>(stg + (32 * j + rr) * 32 + 16 * k);
         const int t = wt * 64 + 32 * j + rr;
-        if (t < valid) *reinterpret_cast<v4u*>(C + (int64_t)(row0 + t) * half + ncol0 + 16 * k) = d;
+        __builtin_amdgcn_raw_buffer_store_b128(d, cr, t * half + ncol0 + 16 * k, 0, 0);
       }
     }
   }
@@ -915,10 +935,11 @@ KERN_DEV RingTile ring_tile(const BmmArgs& A, int nx, int expert, int row0, int 
   T.sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)rg0 * KG) * 256;
   // token (activation row) of tile row t; rows past the slot's last valid row read row/token 0 (their
   // accumulators are never stored)
+  // (FC1: the route_map entry is read for every row, live or not, in bounds as the tables hold max_slots *
+  // 128 rows: a fixed number of loads, which the next k-loop's first wait counts)
   auto token_of = [&](int t) -> int {
-    if (t >= valid) return 0;
-    if (MODE == MODE_FC1) return A.route_map[row0 + t];
-    return row0 + t;
+    const int v = MODE == MODE_FC1 ? A.route_map[row0 + t] : row0 + t;
+    return t >= valid ? 0 : v;
   };
 #pragma unroll
   for (int r = 0; r < 4; ++r) T.xtok[r] = token_of(32 * r + 8 * gw + (lane >> 3));
@@ -1030,9 +1051,11 @@ KERN_DEV void ring_prologue(const BmmArgs& A, const BmmLds& L, const RingTile& T
 // `chain` (Tn is T) they re-read T's last k-tile and scale group instead, so that the counts, and the waits,
 // are the same. Ends with every wave past the tile's last barrier (no wave reads the ring after it); the
 // last requests may still be in flight.
+// first: no epilogue ran since the tile's first requests (ring_prologue); otherwise the tile before's
+// epilogue stores (epi_stores) and, in FC1, Tn's route_map loads (ring_tile: 6) were sent after them.
 template <int MODE>
 KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, const RingTile& Tn, bool chain,
-                         v4f (&acc)[4][4]) {
+                         bool first, v4f (&acc)[4][4]) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1059,12 +1082,21 @@ KERN_DEV void ring_kloop(const BmmArgs& A, const BmmLds& L, const RingTile& T, c
     constexpr int NTS = decltype(NTSc)::value;  // live token subtiles of this wave (uniform)
     constexpr int NXR = decltype(NXRc)::value;  // live 32-row activation blocks (group 1's requests)
     constexpr int NXS = NXR > 2 ? 2 : 1;        // activation-scale requests per k group
-    // k-tile 0 and the scales of k group 0 have landed once only tiles 1..3 (1..2 for activations) and
-    // whatever this wave sent after them (such as the tile before's epilogue stores) are outstanding
-    if (grp == 0)
-      WAIT_VMCNT(12);
-    else
-      WAIT_VMCNT(2 * NXR);
+    // k-tile 0 and the scales of k group 0 have landed once only tiles 1..3 (1..2 for activations; 4
+    // requests each when chained, NXR after ring_prologue) and whatever this wave sent after them are
+    // outstanding: Tn's route_map loads (FC1) and, unless first, the tile before's epilogue stores
+    constexpr int R = MODE == MODE_FC1 ? 6 : 0, ST = epi_stores<MODE>();
+    if (grp == 0) {
+      if (first)
+        WAIT_VMCNT(12 + R);
+      else
+        WAIT_VMCNT(12 + R + ST);
+    } else {
+      if (first)
+        WAIT_VMCNT(2 * NXR + R);
+      else
+        WAIT_VMCNT(8 + R + ST);
+    }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     v4i wa[4];         // W operands of the tile in hand
@@ -1230,7 +1262,7 @@ KERN_DEV void bmm_tile(const BmmArgs& A, const BmmLds& L) {
   const RingTile T = ring_tile<MODE>(A, nx, 0, row0, min(A.rows, row0 + BT) - row0);
   ring_prologue<MODE>(A, L, T);
   v4f acc[4][4];
-  ring_kloop<MODE>(A, L, T, T, false, acc);
+  ring_kloop<MODE>(A, L, T, T, false, true, acc);
   ring_epilogue<MODE>(A, T, acc, L.stg);
   // the last (clamped) requests land before the workgroup's LDS is released
   WAIT_VMCNT(0);
@@ -1425,14 +1457,15 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
       RingTile T = ring_tile<MODE>(A, nx, lexp[0], slot * BT, lval[0]);
       ring_prologue<MODE>(A, L, T);
       for (int e = 0; e < nr; ++e) {
+        // the next tile (this one again after the last, so that its loads are sent all the same)
         const bool chain = e + 1 < nr;
-        RingTile Tn = T;
-        if (chain) {
-          moe_tile(owner(0), list[e + 1], nne, gx, G, nx, slot);
-          Tn = ring_tile<MODE>(A, nx, lexp[e + 1], slot * BT, lval[e + 1]);
-        }
+        const int en = chain ? e + 1 : e;
+        moe_tile(owner(0), list[en], nne, gx, G, nx, slot);
+        const RingTile Tn = ring_tile<MODE>(A, nx, lexp[en], slot * BT, lval[en]);
+        // Tn's loads (FC1's route_map) stay before the k-loop's first wait, which counts them
+        asm volatile("" ::: "memory");
         v4f acc[4][4];
-        ring_kloop<MODE>(A, L, T, Tn, chain, acc);
+        ring_kloop<MODE>(A, L, T, Tn, chain, e == 0, acc);
         ring_epilogue<MODE>(A, T, acc, L.stg);
         T = Tn;
       }
