@@ -408,8 +408,8 @@ extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf
                                                   const int32_t* total_padded, const int32_t* cta_batch,
                                                   const int32_t* cta_limit, int32_t m, int32_t k, int32_t ctas,
                                                   int32_t sf_b_r128c4, float* dbg, void* stream) {
-  REQUIRE(m > 0 && m % 256 == 0 && k > 0 && k % 512 == 0 && ctas >= 0 && ctas < 65536,
-          "trtllm_bmm_bf16_mxe2m1_mxe4m3: need m %% 256 == 0, k %% 512 == 0, 0 <= ctas < 65536 (m=%d k=%d ctas=%d)",
+  REQUIRE(m > 0 && m % 256 == 0 && m <= 131072 && k > 0 && k % 512 == 0 && ctas >= 0 && ctas < 65536,
+          "trtllm_bmm_bf16_mxe2m1_mxe4m3: need m %% 256 == 0, m <= 131072, k %% 512 == 0, 0 <= ctas < 65536 (m=%d k=%d ctas=%d)",
           m, k, ctas);
   REQUIRE(a_ && sf_a && b && sf_b && c && num_non_exiting && total_padded && cta_batch && cta_limit,
           "trtllm_bmm_bf16_mxe2m1_mxe4m3: null buffer");
@@ -426,8 +426,8 @@ extern "C" int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a_, const void* 
                                                     const int32_t* num_non_exiting, const int32_t* total_padded,
                                                     const int32_t* cta_batch, const int32_t* cta_limit, int32_t m,
                                                     int32_t k, int32_t ctas, float* dbg, void* stream) {
-  REQUIRE(m > 0 && m % 256 == 0 && k > 0 && k % 512 == 0 && ctas >= 0 && ctas < 65536,
-          "trtllm_bmm_mxe4m3_mxe2m1_mxe4m3: need m %% 256 == 0, k %% 512 == 0, 0 <= ctas < 65536 (m=%d k=%d ctas=%d)",
+  REQUIRE(m > 0 && m % 256 == 0 && m <= 131072 && k > 0 && k % 512 == 0 && ctas >= 0 && ctas < 65536,
+          "trtllm_bmm_mxe4m3_mxe2m1_mxe4m3: need m %% 256 == 0, m <= 131072, k %% 512 == 0, 0 <= ctas < 65536 (m=%d k=%d ctas=%d)",
           m, k, ctas);
   REQUIRE(a_ && sf_a && b && sf_b && c && sf_c && route_map && alpha && beta && num_non_exiting && total_padded &&
               cta_batch && cta_limit,

@@ -1393,6 +1393,7 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
   const int nne = min(A.num_non_exiting[0], A.max_slots);
   const int gx = A.m >> 8, G = gridDim.x;
   constexpr int kSkinny = skinny_rows<MODE>();
+  if (gx > 512) return;  // the tile lists hold nx < 512 (the host rejects m > 131072)
   // quarter owners: b - o*G/4 (mod G) for o = 0..3 when the launch has at most G/2 live tiles (and G/4 is
   // a multiple of 8), else b for all four quarters. Spreading the small tiles of larger launches cost
   // more than it gained: config 4's FC1 (4096 tiles, half of them small) took 853 us against 712 us with
@@ -1434,17 +1435,17 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
     const unsigned long long below = (1ull << (tp & 63)) - 1ull;
     if (ring) {  // at most 128: o == 0 only
       const int at = pr + __popcll(br & below);
-      list[at] = base + j;
+      list[at] = slot * 512 + nx;  // decoded here once (m <= 512 * 256, checked on the host)
       lexp[at] = ex;
       lval[at] = v;
     }
     if (spread) {
-      if (skin) list[128 + ps + __popcll(bs & below)] = (base + j) * 4 + o;
+      if (skin) list[128 + ps + __popcll(bs & below)] = (slot * 512 + nx) * 4 + o;
     } else {
       // all four thread groups classify the same tiles: quarter o of the r-th small tile goes to 4r + o,
       // so that waves 0-3 take one tile's quarters together and waves 4-7 the next one's
       const int r = ((wave & 1) ? wcnt[8 + wave - 1] : 0) + __popcll(bs & below);
-      if (skin) list[128 + 4 * r + o] = (base + j) * 4 + o;
+      if (skin) list[128 + 4 * r + o] = (slot * 512 + nx) * 4 + o;
       ns = 4 * (wcnt[8] + wcnt[9]);
     }
     // the pass's last candidate of the smallest owner (the first CU of the XCD among the owners) lies past
@@ -1453,15 +1454,14 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
     __syncthreads();
     // the ring tiles, chained: each tile's last k-steps send the next one's first requests (ring_kloop)
     if (nr > 0) {
-      moe_tile(owner(0), list[0], nne, gx, G, nx, slot);
-      RingTile T = ring_tile<MODE>(A, nx, lexp[0], slot * BT, lval[0]);
+      RingTile T = ring_tile<MODE>(A, list[0] & 511, lexp[0], (list[0] >> 9) * BT, lval[0]);
       ring_prologue<MODE>(A, L, T);
       for (int e = 0; e < nr; ++e) {
         // the next tile (this one again after the last, so that its loads are sent all the same)
         const bool chain = e + 1 < nr;
         const int en = chain ? e + 1 : e;
-        moe_tile(owner(0), list[en], nne, gx, G, nx, slot);
-        const RingTile Tn = ring_tile<MODE>(A, nx, lexp[en], slot * BT, lval[en]);
+        const int code = list[en];
+        const RingTile Tn = ring_tile<MODE>(A, code & 511, lexp[en], (code >> 9) * BT, lval[en]);
         // Tn's loads (FC1's route_map) stay before the k-loop's first wait, which counts them
         asm volatile("" ::: "memory");
         v4f acc[4][4];
@@ -1474,7 +1474,7 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
     }
     for (int e = wave; e < ns; e += 8) {
       const int code = list[128 + e], q = code & 3;
-      moe_tile(owner(q), code >> 2, nne, gx, G, nx, slot);
+      nx = (code >> 2) & 511, slot = code >> 11;
       const int row0 = slot * BT, expert = A.cta_batch[slot], valid = A.cta_limit[slot] - row0;
       if (kSkinny <= 16 || valid <= 16)
         skinny_tile<MODE, 1>(A, nx, expert, row0, valid, q, lane);

@@ -106,7 +106,7 @@ def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
     """moe_fc1 = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (13 params); launch adds i32 m (= 2I), i32 k (= H), the slot
     tables' capacity E + ceil(tokens*topk/128) and a null f32 debug pointer (an i64 zero). The kernel is persistent: grid [256, 1, 1], and each workgroup
     loops over the live slots' tiles (num_non_exiting is read on the device), so the grid needs no var."""
-    assert m % 256 == 0 and k % 512 == 0
+    assert m % 256 == 0 and m <= 131072 and k % 512 == 0  # the kernels' tile lists hold m/256 < 512
     p = ["in buffer<u8>"] * 4 + ["out buffer<u8>"] * 2 + ["in buffer<i32>", "in buffer<f32>", "in buffer<f32>"] \
         + ["in buffer<i32>"] * 4
     return {
@@ -126,7 +126,7 @@ def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
     """moe_fc2 = trtllm_bmm_bf16_mxe2m1_mxe4m3 (9 params); launch adds i32 m (= H), i32 k (= I), the slot
     tables' capacity, i32 sf_b_r128c4 = 1 (FC1 writes its scales R128c4) and a null f32 debug pointer.
     Persistent grid as moe_fc1."""
-    assert m % 256 == 0 and k % 512 == 0
+    assert m % 256 == 0 and m <= 131072 and k % 512 == 0  # the kernels' tile lists hold m/256 < 512
     p = ["in buffer<u8>"] * 4 + ["out buffer<bf16>"] + ["in buffer<i32>"] * 4
     return {
         "params": p,
