@@ -1,6 +1,6 @@
 """Benchmark of the MXFP4 matmul path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--decode-m 1 4 16]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--decode-m 1 4 16] [--stack-m 1 64 2048]
                     [--only gemm|decode|moe|stack|mxfp8|k3|peaks|copy]
 
 Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
@@ -93,6 +93,8 @@ def parse():
                          "three plain 256 MiB device copies: the reference for scaling HBM byte counters")
     ap.add_argument("--decode-m", type=int, nargs="+", default=[1, 4, 16],
                     help="token counts of the decode leg (the first one is its headline)")
+    ap.add_argument("--stack-m", type=int, nargs="+", default=list(S_MS),
+                    help="token counts of the config-5 stack leg")
     return ap.parse_args()
 
 
@@ -374,10 +376,10 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
     y = torch.empty((MT, MH), dtype=torch.bfloat16, device="cuda")
     torch.cuda.synchronize()
 
-    def route():
-        ops.moe_quant(x, q, qs, MT, K=MH)
-        ops.moe_routing(ids, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"], tab["total_padded"],
-                        tab["route_map"], tab["exp2perm"], tokens=MT, topk=MTOP, local_start=0, local_experts=ME)
+    def route():  # moe_quant + moe_routing (one launch)
+        ops.moe_quant_routing(x, q, qs, ids, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"],
+                              tab["total_padded"], tab["route_map"], tab["exp2perm"], tokens=MT, K=MH, topk=MTOP,
+                              local_start=0, local_experts=ME)
 
     def fc1():
         ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(w1, s1, q, qs, c1, sf1, tab["route_map"], alpha, beta, tab["nne"],
@@ -414,7 +416,7 @@ def bench_moe(torch, ops, wl, stream, steps, warmup):
             "slots": ctas, "samples": samples}
 
 
-def bench_stack(torch, ops, wl, stream, steps, warmup):
+def bench_stack(torch, ops, wl, stream, steps, warmup, ms_list=S_MS):
     """Config 5: the layer stack at each M, one hipGraph per M captured through kern_graph_*."""
     u8, i32, bf16 = torch.uint8, torch.int32, torch.bfloat16
     H, I, E, k = MH, MI, ME, MTOP
@@ -448,7 +450,7 @@ def bench_stack(torch, ops, wl, stream, steps, warmup):
     per_expert = 2 * I * H * 17 // 32 + H * I * 17 // 32
     w_dense = S_QKV * H * 17 // 32 + H * S_OIN * 17 // 32
     res = {}
-    for M in S_MS:
+    for M in ms_list:
         ids_np = [wl.topk_ids(540 + l + 10 * M, M, E, k) for l in range(S_LAYERS)]
         ids = [torch.from_numpy(a).cuda() for a in ids_np]
         tw = dev_from_np(wl.topk_weights(560 + M, M, k), torch)
@@ -482,10 +484,10 @@ def bench_stack(torch, ops, wl, stream, steps, warmup):
                     ops.mxfp4_gemm_bf16(*L["qkv"], xq, xqs, qkv, M=M, m=S_QKV, k=H)
                     ops.moe_quant(attn, aq, aqs, M, K=S_OIN)
                     ops.mxfp4_gemm_bf16(*L["o"], aq, aqs, o[l], M=M, m=H, k=S_OIN)
-                ops.moe_quant(o[l], xq, xqs, M, K=H)
-                ops.moe_routing(ids[l], tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"],
-                                tab["total_padded"], tab["route_map"], tab["exp2perm"], tokens=M, topk=k,
-                                local_start=0, local_experts=E)
+                # moe_quant + moe_routing (one launch up to 255 quantizer workgroups, else two)
+                ops.moe_quant_routing(o[l], xq, xqs, ids[l], tab["counts"], tab["cta_batch"], tab["cta_limit"],
+                                      tab["nne"], tab["total_padded"], tab["route_map"], tab["exp2perm"], tokens=M,
+                                      K=H, topk=k, local_start=0, local_experts=E)
                 ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(*L["w13"], xq, xqs, c1, sf1, tab["route_map"], alpha, beta,
                                                     tab["nne"], tab["total_padded"], tab["cta_batch"],
                                                     tab["cta_limit"], m=2 * I, k=H, ctas=ctas)
@@ -699,7 +701,7 @@ def main():
         torch.cuda.synchronize()
         st = None
         if args.only in (None, "stack"):
-            st = bench_stack(torch, ops, wl, stream, args.steps, args.warmup)
+            st = bench_stack(torch, ops, wl, stream, args.steps, args.warmup, args.stack_m)
         torch.cuda.synchronize()
         m8 = None
         if args.only in (None, "mxfp8"):

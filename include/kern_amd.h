@@ -261,6 +261,17 @@ int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_t* cta_batc
                      int32_t* num_non_exiting, int32_t* total_padded, int32_t* route_map, int32_t* exp2perm,
                      int32_t tokens, int32_t topk, int32_t local_start, int32_t local_experts, void* stream);
 
+/* moe_quant and moe_routing in one call: the outputs of kern_moe_quant(x, q, sf, tokens, K) and of
+ * kern_moe_routing(topk_idx, ..., tokens, topk, local_start, local_experts), bit for bit, with the same
+ * argument rules. No counterpart in the reference, which runs the two ops (head.json:25057, :25117) as
+ * two launches: for callers that run both back to back on the same tokens, such as a decode step, where
+ * each launch is mostly launch and memory latency. One launch when the quantizer needs at most 255
+ * workgroups of 1024 lanes (tokens * K <= 4,177,920), else the two launches. */
+int kern_moe_quant_routing(const void* x, void* q, void* sf, int32_t tokens, int32_t K, const int32_t* topk_idx,
+                           int32_t* counts, int32_t* cta_batch, int32_t* cta_limit, int32_t* num_non_exiting,
+                           int32_t* total_padded, int32_t* route_map, int32_t* exp2perm, int32_t topk,
+                           int32_t local_start, int32_t local_experts, void* stream);
+
 /* trtllm_bmm_bf16_mxe2m1_mxe4m3 = moe_fc2 (head.json:25683; interface trtllm_bmm.py:19-27):
  * a u8 [E][m][k/2] repacked MXFP4, sf_a repacked, b u8 [rows][k] e4m3, sf_b (R128c4 over rows when
  * sf_b_r128c4, else linear [rows][k/32]), c bf16 [rows][m], num_non_exiting, total_padded, cta_batch,

@@ -57,6 +57,8 @@ ENTRIES = {
     "kern_mx_gemm_bf16": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
                           "i32", "i32", "i32", "out buffer<f32>"],
     "kern_mx_routing": ["in buffer<i32>"] + ["out buffer<i32>"] * 7 + ["i32"] * 4,
+    "kern_mx_quant_routing": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "in buffer<i32>"] +
+                             ["out buffer<i32>"] * 7 + ["i32"] * 4,
     "kern_mx_fill_random_u8": ["out buffer<u8>", "i64", "u64", "i32", "i32"],
     "kern_silu_mul_bf16": ["out buffer<bf16>", "in buffer<bf16>", "i32"],
     "kern_mx_moe_finalize_rms": ["in buffer<bf16>", "in buffer<i32>", "in buffer<f32>", "in buffer<bf16>",

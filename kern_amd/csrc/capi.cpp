@@ -403,6 +403,34 @@ extern "C" int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_
   return launch("kern_mx_routing", 1, 1, 1, 1024, stream, a);
 }
 
+extern "C" int kern_moe_quant_routing(const void* x, void* q, void* sf, int32_t tokens, int32_t K,
+                                      const int32_t* topk_idx, int32_t* counts, int32_t* cta_batch,
+                                      int32_t* cta_limit, int32_t* num_non_exiting, int32_t* total_padded,
+                                      int32_t* route_map, int32_t* exp2perm, int32_t topk, int32_t local_start,
+                                      int32_t local_experts, void* stream) {
+  REQUIRE(tokens >= 0 && K > 0 && K % 32 == 0, "moe_quant_routing: need K %% 32 == 0 and tokens >= 0 (K=%d tokens=%d)",
+          K, tokens);
+  REQUIRE(topk > 0 && local_experts > 0 && local_experts <= 512 && local_start >= 0,
+          "moe_quant_routing: need topk > 0, 0 < local_experts <= 512 (got %d, %d)", topk, local_experts);
+  REQUIRE(topk_idx && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm,
+          "moe_quant_routing: null buffer");
+  REQUIRE(tokens == 0 || (x && q && sf), "moe_quant_routing: null buffer");
+  // quantizer workgroups of 1024 lanes (16 elements a lane); the routing block's LDS holds every workgroup
+  // of the launch to one per CU, so the fused launch is taken when all of them fit in one round
+  const int64_t qwg = ((int64_t)tokens * (K / 16) + 1023) / 1024;
+  if (qwg > 255) {
+    const int rc = kern_moe_routing(topk_idx, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map,
+                                    exp2perm, tokens, topk, local_start, local_experts, stream);
+    if (rc != KERN_OK) return rc;
+    return kern_moe_quant(x, q, sf, tokens, K, stream);
+  }
+  Args a;
+  a.put(x), a.put(q), a.put(sf), a.put(K), a.put(topk_idx), a.put(counts), a.put(cta_batch), a.put(cta_limit);
+  a.put(num_non_exiting), a.put(total_padded), a.put(route_map), a.put(exp2perm), a.put(tokens), a.put(topk);
+  a.put(local_start), a.put(local_experts);
+  return launch("kern_mx_quant_routing", (uint32_t)(1 + qwg), 1, 1, 1024, stream, a);
+}
+
 extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf_a, const void* b, const void* sf_b,
                                                   void* c, const int32_t* num_non_exiting,
                                                   const int32_t* total_padded, const int32_t* cta_batch,

@@ -23,13 +23,12 @@ struct IC { static constexpr int value = V; };
 // launch i32 K. Two lanes per 32-element block, 16 elements (two 16-byte loads) per lane, so a wave-wide
 // load covers 1 KiB of contiguous input and each 16-byte store 1 KiB of output; the block amax is
 // reduced over the lane pair with DPP. A workgroup covers 4096 elements: grid ceil(T*K / 4096), block 256.
-extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint16_t* __restrict__ x,
-                                                                     uint8_t* __restrict__ q,
-                                                                     uint8_t* __restrict__ sf, int T, int K) {
+// Lane p of the launch (p even on even lanes) takes elements [16p, 16p + 16).
+KERN_DEV void quant_bf16_lane(const uint16_t* __restrict__ x, uint8_t* __restrict__ q, uint8_t* __restrict__ sf, int T,
+                              int K, int64_t p) {
   // a lane takes 16 adjacent elements (half a 32-element block), a lane pair one block: one cross-lane step
   // for the block's amax, one 16-byte store. (8 elements per lane, four lanes per block, two chunks per
   // lane: 3% slower at config 3's activations; more than one pair per lane was slower still.)
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t np = (int64_t)T * (K >> 4);
   // a lane pair is in or out of range together (K % 32 == 0: np is even)
   if (p >= np) return;
@@ -49,7 +48,12 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint1
   out[2] = mx_pack4(v1[0], v1[1], sc);
   out[3] = mx_pack4(v1[2], v1[3], sc);
   reinterpret_cast<v4u*>(q)[p] = out;
-  if ((threadIdx.x & 1) == 0) sf[p >> 1] = (uint8_t)sc;
+  if ((threadIdx.x & 1) == 0) sf[p >> 1] = (uint8_t)sc;  // p and the lane have the same parity
+}
+extern "C" __global__ __launch_bounds__(256) void kern_mx_quant_bf16(const uint16_t* __restrict__ x,
+                                                                     uint8_t* __restrict__ q,
+                                                                     uint8_t* __restrict__ sf, int T, int K) {
+  quant_bf16_lane(x, q, sf, T, K, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
 // f32 -> MXFP8 with the codec of the FC1 epilogue (mx_scale_code of the block's largest |bits|, then
@@ -1789,10 +1793,10 @@ KERN_DEV int wave_incl_scan(int v, int lane) {
   return v;
 }
 
-extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
-    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
-    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
-    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+KERN_DEV void routing_block(const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+                           int* __restrict__ cta_limit, int* __restrict__ num_non_exiting,
+                           int* __restrict__ total_padded, int* __restrict__ route_map, int* __restrict__ exp2perm,
+                           int T, int topk, int local_start, int E_local) {
   __shared__ int wbase[16 * ROUTE_EMAX];                 // [wave][expert]: count, then the wave's next row
   __shared__ unsigned long long wmask[16 * ROUTE_EMAX];  // [wave][expert]: lanes holding the expert
   __shared__ int off[ROUTE_EMAX];                        // per-expert first slot
@@ -1875,6 +1879,32 @@ extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
     }
   }
 }
+
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
+    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
+    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+  routing_block(topk_idx, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, T, topk,
+                local_start, E_local);
+}
+
+// moe_quant and moe_routing in one launch (they are independent): workgroup 0 builds the routing tables
+// (kern_mx_routing's block), workgroups 1.. quantize (kern_mx_quant_bf16's lanes, 1024 per workgroup). For
+// decode-sized batches, where each of the two launches is mostly launch and memory latency. Grid
+// 1 + ceil(T*K/16 / 1024), block 1024.
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_quant_routing(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q, uint8_t* __restrict__ sf, int K,
+    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
+    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+  if (blockIdx.x == 0) {
+    routing_block(topk_idx, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, T, topk,
+                  local_start, E_local);
+    return;
+  }
+  quant_bf16_lane(x, q, sf, T, K, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
+}
+
 
 // ====================================================================================== MoE glue
 // silu_mul (tools/kernels-src/silu_mul.cu:1-5): out[t][i] = bf16(bf16(g / (1 + exp(-g))) * u), g = in[t][i],

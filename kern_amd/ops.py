@@ -43,6 +43,7 @@ _SIGS = {
     "kern_moe_w_shuffle": [P, P, I32, I32, I32, I32, P],
     "kern_moe_sf_shuffle": [P, P, I32, I32, I32, I32, P],
     "kern_moe_routing": [P] * 8 + [I32] * 4 + [P],
+    "kern_moe_quant_routing": [P, P, P, I32, I32] + [P] * 8 + [I32] * 3 + [P],
     "kern_trtllm_bmm_bf16_mxe2m1_mxe4m3": [P] * 9 + [I32, I32, I32, I32, P, P],
     "kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3": [P] * 13 + [I32, I32, I32, P, P],
     "kern_mxfp4_gemm_e4m3": [P] * 6 + [I32, I32, I32, P, P],
@@ -202,6 +203,20 @@ def moe_routing(topk_idx, counts, cta_batch, cta_limit, num_non_exiting, total_p
         _ptr(num_non_exiting, "num_non_exiting", i32, 1), _ptr(total_padded, "total_padded", i32, 1),
         _ptr(route_map, "route_map", i32, ctas * 128), _ptr(exp2perm, "exp2perm", i32, tokens * topk),
         tokens, topk, local_start, local_experts, _stream()))
+
+
+def moe_quant_routing(x, q, sf, topk_idx, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map,
+                      exp2perm, *, tokens, K, topk, local_start, local_experts):
+    """moe_quant and moe_routing in one call (one launch for decode-sized batches): the outputs of
+    moe_quant(x, q, sf, tokens, K=K) and moe_routing(topk_idx, ..., tokens=tokens, topk=topk, ...)."""
+    ctas = ctas_bound(tokens, topk, local_experts)
+    check(lib().kern_moe_quant_routing(
+        _ptr(x, "x", bf16, tokens * K), _ptr(q, "q", u8, tokens * K), _ptr(sf, "sf", u8, tokens * K // 32), tokens, K,
+        _ptr(topk_idx, "topk_idx", i32, tokens * topk), _ptr(counts, "counts", i32, 2 * local_experts),
+        _ptr(cta_batch, "cta_batch", i32, ctas), _ptr(cta_limit, "cta_limit", i32, ctas),
+        _ptr(num_non_exiting, "num_non_exiting", i32, 1), _ptr(total_padded, "total_padded", i32, 1),
+        _ptr(route_map, "route_map", i32, ctas * 128), _ptr(exp2perm, "exp2perm", i32, tokens * topk),
+        topk, local_start, local_experts, _stream()))
 
 
 def trtllm_bmm_bf16_mxe2m1_mxe4m3(a, sf_a, b, sf_b, c, num_non_exiting, total_padded, cta_batch, cta_limit, *, m, k,

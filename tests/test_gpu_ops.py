@@ -208,6 +208,40 @@ def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
     np.testing.assert_array_equal(to_np(dev["exp2perm"]), ref["exp2perm"].reshape(-1))
 
 
+# moe_quant + moe_routing in one call: decode sizes and config 4 in one launch; a K3 rank's local experts
+# (ids outside the range); T*K past one launch's quantizer workgroups, which takes the two launches
+@pytest.mark.parametrize("T,E,k,start,local,K", [(1, 256, 8, 0, 256, 7168), (4, 256, 8, 0, 256, 7168),
+                                                 (64, 256, 8, 0, 256, 7168), (512, 256, 8, 0, 256, 7168),
+                                                 (300, 224, 16, 56, 56, 3584), (600, 256, 8, 0, 256, 7168),
+                                                 (3, 8, 2, 0, 8, 96)])
+def test_quant_routing_fused(ops, oracle, T, E, k, start, local, K):
+    x = wl.activations_bf16(11 + T, T, K, outlier_frac=0.01)
+    x[:min(T, 8)] = _special_rows(K)[:min(T, 8)]
+    ids = wl.topk_ids(T * 7 + E, T, E, k)
+    ctas = ops.ctas_bound(T, k, local)
+    ref = oracle.routing(ids, start, local, ctas_cap=ctas)
+    q_ref, sf_ref = oracle.quant_mxfp8(x)
+    dev = {n: torch.full((s,), -7, dtype=torch.int32, device="cuda") for n, s in
+           [("counts", 2 * local), ("cta_batch", ctas), ("cta_limit", ctas), ("num_non_exiting", 1),
+            ("total_padded", 1), ("route_map", ctas * 128), ("exp2perm", T * k)]}
+    q = torch.full((T, K), 0x5A, dtype=torch.uint8, device="cuda")
+    sf = torch.full((T, K // 32), 0x5A, dtype=torch.uint8, device="cuda")
+    ops.moe_quant_routing(to_dev(x), q, sf, to_dev(ids), dev["counts"], dev["cta_batch"],
+                          dev["cta_limit"], dev["num_non_exiting"], dev["total_padded"], dev["route_map"],
+                          dev["exp2perm"], tokens=T, K=K, topk=k, local_start=start, local_experts=local)
+    _sync()
+    np.testing.assert_array_equal(to_np(sf), sf_ref)
+    np.testing.assert_array_equal(to_np(q), q_ref)
+    S = int(ref["num_non_exiting"][0])
+    assert int(to_np(dev["num_non_exiting"])[0]) == S
+    assert int(to_np(dev["total_padded"])[0]) == S * 128
+    np.testing.assert_array_equal(to_np(dev["counts"]), ref["counts"])
+    np.testing.assert_array_equal(to_np(dev["cta_batch"])[:S], ref["cta_batch"][:S])
+    np.testing.assert_array_equal(to_np(dev["cta_limit"])[:S], ref["cta_limit"][:S])
+    np.testing.assert_array_equal(to_np(dev["route_map"])[:S * 128], ref["route_map"][:S * 128])
+    np.testing.assert_array_equal(to_np(dev["exp2perm"]), ref["exp2perm"].reshape(-1))
+
+
 # --------------------------------------------------------------------------------------- grouped FC1 / FC2
 
 def _route(ops, oracle, ids, local_start, local):
