@@ -773,7 +773,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     uint8_t* C = reinterpret_cast<uint8_t*>(A.c);
     const int half = m >> 1;
     const float al = A.alpha[expert], be = A.beta[expert];
-    const float ial = 1.0f / al, ibe = 1.0f / be, albe = al * be;
+    const SituCoef G = situ_coef(al), U = situ_coef(be);  // SiTU's per-expert coefficient sets
     // the wave's 64 interleaved gate/up rows give 32 output columns: one MXFP8 block
     const int ncol0 = (nx * BN + wn * 64) >> 1;
     const int blk = ncol0 >> 5;
@@ -790,7 +790,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
         const v4f v = acc[ts][rs];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          h[rs][i] = situ_fast(v[i], v[i + 2], ial, ibe, albe);
+          h[rs][i] = situ_fast(v[i], v[i + 2], G, U);
         }
       }
       const bool ok = t < valid;

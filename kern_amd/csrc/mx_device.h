@@ -146,37 +146,59 @@ KERN_DEV uint32_t mx_code2(float a, float b, uint32_t sc) {
   return e4m3_hw2(__builtin_ldexpf(a, sh), __builtin_ldexpf(b, sh));
 }
 
-// tanh(x) as num / den = a P(a^2) / Q(a^2), a = x clamped to [-9, 9] (past 9, tanh is 1 to within half an
-// f32 ulp), with P and Q of degree 4 in a^2 and Q(0) = P(0) = 1: a minimax fit of the relative error made for
-// this kernel (linear programming on a dense grid of [0, 9] with Loeb reweighting; largest relative error of
-// num/den 7.3e-8 in exact arithmetic, 2.9e-7 with this f32 evaluation). Eight FMAs and no transcendental, so
-// that SiTU-GLU below needs one exponential and one reciprocal in all. The clamp propagates NaN.
-KERN_DEV void tanh_pq(float x, float& num, float& den) {
-  const float a = __builtin_elementwise_minimum(__builtin_elementwise_maximum(x, -9.0f), 9.0f);
+// alpha * tanh(x / alpha) as num / den = a P(a^2) / Q(a^2), a = x clamped to [-8 alpha, 8 alpha] (past 8,
+// tanh is 1 to within 2.3e-7): tanh(y) ~ y p(y^2) / q(y^2) with p of degree 3 and q of degree 4 (q(0) = 1), a
+// minimax fit of the relative error made for this kernel (linear programming on a dense grid of [0, 8] with
+// Loeb reweighting; 1.7e-7 in exact arithmetic, 4.0e-7 with an f32 evaluation). Its coefficients are scaled
+// once per expert (SituCoef: the coefficient of y^2k times alpha^-2k, so P(a^2) = p(y^2) for a = alpha y):
+// no multiply by 1/alpha, and the alpha of alpha * tanh cancels the 1/alpha of y. Seven FMAs and no
+// transcendental, so that SiTU-GLU below needs one exponential and one reciprocal in all. The clamp
+// propagates NaN.
+struct SituCoef {
+  float p1, p2, p3, q1, q2, q3, q4, c;  // wave-uniform (kept in SGPRs)
+};
+KERN_DEV float uniform_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+KERN_DEV SituCoef situ_coef(float alpha) {
+  const float ia = 1.0f / alpha, i2 = ia * ia;
+  SituCoef C;
+  float sc = i2;
+  C.p1 = uniform_f32(1.292369813e-01f * sc), C.q1 = uniform_f32(4.625690877e-01f * sc);
+  sc *= i2;
+  C.p2 = uniform_f32(2.948877867e-03f * sc), C.q2 = uniform_f32(2.380688488e-02f * sc);
+  sc *= i2;
+  C.p3 = uniform_f32(1.140421136e-05f * sc), C.q3 = uniform_f32(2.383597312e-04f * sc);
+  sc *= i2;
+  C.q4 = uniform_f32(2.451302805e-07f * sc);
+  C.c = uniform_f32(8.0f * alpha);
+  return C;
+}
+KERN_DEV void tanh_pq(float x, const SituCoef& C, float& num, float& den) {
+  const float a = __builtin_elementwise_minimum(__builtin_elementwise_maximum(x, -C.c), C.c);
   const float s = a * a;
-  float p = __builtin_fmaf(s, 1.249417281e-08f, 1.994559352e-05f);
-  p = __builtin_fmaf(p, s, 3.453583224e-03f);
-  p = __builtin_fmaf(p, s, 1.334516704e-01f);
-  p = __builtin_fmaf(p, s, 1.0f);
-  float q = __builtin_fmaf(s, 7.411605907e-07f, 3.218087368e-04f);
-  q = __builtin_fmaf(q, s, 2.571561001e-02f);
-  q = __builtin_fmaf(q, s, 4.667846560e-01f);
+  float p = __builtin_fmaf(s, C.p3, C.p2);
+  p = __builtin_fmaf(p, s, C.p1);
+  p = __builtin_fmaf(p, s, 9.999998808e-01f);
+  float q = __builtin_fmaf(s, C.q4, C.q3);
+  q = __builtin_fmaf(q, s, C.q2);
+  q = __builtin_fmaf(q, s, C.q1);
   q = __builtin_fmaf(q, s, 1.0f);
   num = a * p;
   den = q;
 }
 
 // SiTU-GLU (tools/trtllm-bmm/probe.py:23, :46-47) of gate g and up u, alpha * tanh(g / alpha) * sigmoid(g) *
-// beta * tanh(u / beta), given ial = 1/alpha, ibe = 1/beta and albe = alpha * beta, as one fraction:
-// albe * na * nb / (da * db * (1 + exp(-g))) with tanh = n / d from tanh_pq. One exponential and one hardware
-// reciprocal, no divides. Where exp(-g) or the denominator overflows (g below about -76, sigmoid(g) < 1e-33)
-// the value is 0; NaN in g or u gives NaN.
-KERN_DEV float situ_fast(float g, float u, float ial, float ibe, float albe) {
+// beta * tanh(u / beta), with G = situ_coef(alpha) and U = situ_coef(beta), as one fraction:
+// na * nb / (da * db * (1 + exp(-g))) with alpha * tanh = na / da and beta * tanh = nb / db from tanh_pq. One
+// exponential and one hardware reciprocal, no divides. Where exp(-g) or the denominator overflows (g below
+// about -76, sigmoid(g) < 1e-33) the value is 0; NaN in g or u gives NaN.
+KERN_DEV float situ_fast(float g, float u, const SituCoef& G, const SituCoef& U) {
   float na, da, nb, db;
-  tanh_pq(g * ial, na, da);
-  tanh_pq(u * ibe, nb, db);
+  tanh_pq(g, G, na, da);
+  tanh_pq(u, U, nb, db);
   const float d = da * db;
-  return (albe * na * nb) * __builtin_amdgcn_rcpf(__builtin_fmaf(d, __expf(-g), d));
+  return (na * nb) * __builtin_amdgcn_rcpf(__builtin_fmaf(d, __expf(-g), d));
 }
 
 // f32 value 2^(code-127) (code 0 is the subnormal 2^-127, 255 is NaN)
