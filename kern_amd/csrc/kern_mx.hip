@@ -679,7 +679,9 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       }
     }
     if (STAGED) {
-      // one 16-row subtile at a time: row r (128 B, 64 bf16) at r * 128, 16-byte unit k at ((k ^ (r & 7)) << 4)
+      // one 16-row subtile at a time: row r (128 B, 64 bf16) at r * 128, 16-byte unit k at ((k ^ (r & 7)) << 4),
+      // the unit's two 8-byte halves swapped in rows 8..15, so that the 16 lanes of each g write 16 distinct
+      // bank pairs (rows r and r + 8 would otherwise share them)
       const int rr = lane >> 3, k = lane & 7;
       const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(C + (int64_t)row0 * m), (short)0, max(valid, 0) * m * 2, 0x00020000);
@@ -689,13 +691,14 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
         for (int rs = 0; rs < 4; ++rs) {
           const v4f v = acc[ts][rs];
           const int kw = 2 * rs + (g >> 1);
-          *reinterpret_cast<uint2*>(stg + c * 128 + ((kw ^ (c & 7)) << 4) + 8 * (g & 1)) =
+          *reinterpret_cast<uint2*>(stg + c * 128 + ((kw ^ (c & 7)) << 4) + 8 * ((g & 1) ^ (c >> 3))) =
               make_uint2(bf16x2_hw(v[0], v[1]), bf16x2_hw(v[2], v[3]));
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int r = 8 * h + rr;
-          const v4u d = *reinterpret_cast<const v4u*>(stg + r * 128 + ((k ^ (r & 7)) << 4));
+          v4u d = *reinterpret_cast<const v4u*>(stg + r * 128 + ((k ^ (r & 7)) << 4));
+          if (h) d = d.zwxy;
           const int t = wt * 64 + 16 * ts + r;
           __builtin_amdgcn_raw_buffer_store_b128(d, cr, (t * m + wrow0 + 8 * k) * 2, 0, 0);
         }
@@ -731,7 +734,8 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     }
     if (STAGED) {
       // two 16-row subtiles at a time, subtile ts at (ts & 1) * 1024: row r (64 B, 64 e4m3) at r * 64, 16-byte
-      // unit k at ((k ^ (r & 3)) << 4)
+      // unit k at ((k ^ ((r >> 1) & 3)) << 4), the unit's two 8-byte halves swapped in rows 8..15: the 32 lanes
+      // of each half-wave then write 32 distinct banks
       const int rr = lane >> 2, k = lane & 3;
       const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(C + (int64_t)row0 * m), (short)0, max(valid, 0) * m, 0x00020000);
@@ -742,13 +746,15 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
 #pragma unroll
           for (int rs = 0; rs < 4; ++rs) {
             const v4f v = acc[ts][rs];
-            *reinterpret_cast<uint32_t*>(stg + (ts & 1) * 1024 + c * 64 + ((rs ^ (c & 3)) << 4) + 4 * g) =
+            *reinterpret_cast<uint32_t*>(stg + (ts & 1) * 1024 + c * 64 + ((rs ^ ((c >> 1) & 3)) << 4) +
+                                         4 * (g ^ ((c >> 2) & 2))) =
                 e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
           }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const v4u d = *reinterpret_cast<const v4u*>(stg + j * 1024 + rr * 64 + ((k ^ (rr & 3)) << 4));
+          v4u d = *reinterpret_cast<const v4u*>(stg + j * 1024 + rr * 64 + ((k ^ ((rr >> 1) & 3)) << 4));
+          if (rr >= 8) d = d.zwxy;
           const int t = wt * 64 + 16 * (2 * q + j) + rr;
           __builtin_amdgcn_raw_buffer_store_b128(d, cr, t * m + wrow0 + 16 * k, 0, 0);
         }
