@@ -786,6 +786,9 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
     // sf_c: R128c4 over the tables' max_slots * 128 rows
     const __amdgpu_buffer_rsrc_t sfr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)A.sf_c, (short)0, A.max_slots * ((((half >> 5) + 3) >> 2) * 512), 0x00020000);
+    // a ring tile's row0 is its slot's first row, a multiple of 128: row p = row0 + t has p >> 7 = row0 >> 7
+    // and p & 127 = t, so its R128c4 byte is at sf_base + (t & 31) * 16 + (t >> 5) * 4
+    const int sf_base = 512 * ((row0 >> 7) * ((((half >> 5) + 3) >> 2)) + (blk >> 2)) + (blk & 3);
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       const int t = wt * 64 + ts * 16 + c;
@@ -817,28 +820,27 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       for (int rs = 0; rs < 4; ++rs)
 #pragma unroll
         for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[rs][i]) & 0x7fffffffu);
-      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 16));
-      amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
+      amax = max_over_rows(amax);
       const uint32_t sc = mx_scale_code(amax);
       if (STAGED) {
         // wave row r (32 B: the wave's MXFP8 block of the row) at r * 32
         uint8_t* pc = stg + (16 * ts + c) * 32 + 2 * g;
+        uint32_t o[4];
+        mx_code2x4(h, sc, o);
 #pragma unroll
-        for (int rs = 0; rs < 4; ++rs) *reinterpret_cast<uint16_t*>(pc + 8 * rs) = (uint16_t)mx_code2(h[rs][0], h[rs][1], sc);
+        for (int rs = 0; rs < 4; ++rs) *reinterpret_cast<uint16_t*>(pc + 8 * rs) = (uint16_t)o[rs];
       } else if (ok) {
+        uint32_t o[4];
+        mx_code2x4(h, sc, o);
 #pragma unroll
-        for (int rs = 0; rs < 4; ++rs) {
-          const int n = ncol0 + 8 * rs + 2 * g;
-          const uint32_t o = mx_code2(h[rs][0], h[rs][1], sc);
-          *reinterpret_cast<uint16_t*>(C + p * half + n) = (uint16_t)o;
-        }
+        for (int rs = 0; rs < 4; ++rs)
+          *reinterpret_cast<uint16_t*>(C + p * half + ncol0 + 8 * rs + 2 * g) = (uint16_t)o[rs];
       }
       if (STAGED) {
         // one byte store per subtile from every lane, the lanes other than g = 0 and the rows past the
         // tile's live ones pointed past the end of sf_c (dropped)
-        const int64_t kb4 = ((half >> 5) + 3) >> 2;
-        const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
-        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)sc, sfr, ok && g == 0 ? (int)off : 0x7fffff00, 0, 0);
+        const int off = sf_base + (t & 31) * 16 + (t >> 5) * 4;
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)sc, sfr, ok && g == 0 ? off : 0x7fffff00, 0, 0);
       } else if (ok && g == 0) {
         const int64_t kb4 = ((half >> 5) + 3) >> 2;
         const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);

@@ -146,6 +146,35 @@ KERN_DEV uint32_t mx_code2(float a, float b, uint32_t sc) {
   return e4m3_hw2(__builtin_ldexpf(a, sh), __builtin_ldexpf(b, sh));
 }
 
+// max of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four 16-lane rows of the wave), by the two
+// row-swapping moves (V_PERMLANE32_SWAP, V_PERMLANE16_SWAP): no LDS round trip
+KERN_DEV uint32_t max_over_rows(uint32_t v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  v = max((uint32_t)p[0], (uint32_t)p[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return max((uint32_t)q[0], (uint32_t)q[1]);
+}
+
+// mx_code2 of the four pairs of one lane's share of a block, with one test of the block's scale code: every
+// element of a block with sc < 255 is finite (the largest |bits| is below 0x7f800000), so the conversions
+// need no NaN handling; a non-finite block (sc == 255) gets 0x7f|sign for every element. Same codes as
+// mx_code2 pair by pair.
+KERN_DEV void mx_code2x4(const float (&h)[4][2], uint32_t sc, uint32_t (&o)[4]) {
+  const int sh = 127 - (int)sc;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float a = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(h[r][0], sh), -448.0f), 448.0f);
+    const float b = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(h[r][1], sh), -448.0f), 448.0f);
+    o[r] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+  }
+  if (sc == 255u) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      o[r] = (((__float_as_uint(h[r][0]) >> 24) & 0x80u) | 0x7fu) |
+             ((((__float_as_uint(h[r][1]) >> 24) & 0x80u) | 0x7fu) << 8);
+  }
+}
+
 // alpha * tanh(x / alpha) as num / den = a P(a^2) / Q(a^2), a = x clamped to [-8 alpha, 8 alpha] (past 8,
 // tanh is 1 to within 2.3e-7): tanh(y) ~ y p(y^2) / q(y^2) with p of degree 3 and q of degree 4 (q(0) = 1), a
 // minimax fit of the relative error made for this kernel (linear programming on a dense grid of [0, 8] with
@@ -174,8 +203,7 @@ KERN_DEV SituCoef situ_coef(float alpha) {
   C.c = uniform_f32(8.0f * alpha);
   return C;
 }
-KERN_DEV void tanh_pq(float x, const SituCoef& C, float& num, float& den) {
-  const float a = __builtin_elementwise_minimum(__builtin_elementwise_maximum(x, -C.c), C.c);
+KERN_DEV void tanh_pq_clamped(float a, const SituCoef& C, float& num, float& den) {
   const float s = a * a;
   float p = __builtin_fmaf(s, C.p3, C.p2);
   p = __builtin_fmaf(p, s, C.p1);
@@ -187,6 +215,9 @@ KERN_DEV void tanh_pq(float x, const SituCoef& C, float& num, float& den) {
   num = a * p;
   den = q;
 }
+KERN_DEV void tanh_pq(float x, const SituCoef& C, float& num, float& den) {
+  tanh_pq_clamped(__builtin_elementwise_minimum(__builtin_elementwise_maximum(x, -C.c), C.c), C, num, den);
+}
 
 // SiTU-GLU (tools/trtllm-bmm/probe.py:23, :46-47) of gate g and up u, alpha * tanh(g / alpha) * sigmoid(g) *
 // beta * tanh(u / beta), with G = situ_coef(alpha) and U = situ_coef(beta), as one fraction:
@@ -195,7 +226,8 @@ KERN_DEV void tanh_pq(float x, const SituCoef& C, float& num, float& den) {
 // about -76, sigmoid(g) < 1e-33) the value is 0; NaN in g or u gives NaN.
 KERN_DEV float situ_fast(float g, float u, const SituCoef& G, const SituCoef& U) {
   float na, da, nb, db;
-  tanh_pq(g, G, na, da);
+  // the gate's clamp need not keep a NaN (V_MED3_F32, one instruction): exp(-g) carries it into the result
+  tanh_pq_clamped(__builtin_amdgcn_fmed3f(g, -G.c, G.c), G, na, da);
   tanh_pq(u, U, nb, db);
   const float d = da * db;
   return (na * nb) * __builtin_amdgcn_rcpf(__builtin_fmaf(d, __expf(-g), d));

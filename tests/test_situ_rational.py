@@ -1,4 +1,4 @@
-"""The FC1 epilogue's SiTU-GLU approximation (kern_amd/csrc/mx_device.h: situ_coef, tanh_pq, situ_fast),
+"""The FC1 epilogue's SiTU-GLU approximation (kern_amd/csrc/mx_device.h: situ_coef, tanh_pq_clamped, situ_fast),
 emulated step by step in f32 with the coefficients read from that source file, against the float64 formula
 alpha*tanh(g/alpha)*sigmoid(g)*beta*tanh(u/beta) (tools/trtllm-bmm/probe.py:23, :46-47). The GPU tests bound the
 device's values at 2e-5 relative on every routed row; this pins the approximation's own error well inside that,
@@ -15,10 +15,10 @@ f = np.float32
 
 def _coefficients():
     src = open(SRC).read()
-    coef = src[src.index("KERN_DEV SituCoef situ_coef("):src.index("KERN_DEV void tanh_pq(")]
+    coef = src[src.index("KERN_DEV SituCoef situ_coef("):src.index("KERN_DEV void tanh_pq_clamped(")]
     lit = lambda name: f(re.search(rf"C\.{name} = uniform_f32\(([0-9.e+-]+)f \* sc\)", coef).group(1))
     clamp = f(re.search(r"C\.c = uniform_f32\(([0-9.e+-]+)f \* alpha\)", coef).group(1))
-    body = src[src.index("KERN_DEV void tanh_pq("):src.index("KERN_DEV float situ_fast(")]
+    body = src[src.index("KERN_DEV void tanh_pq_clamped("):src.index("KERN_DEV float situ_fast(")]
     p0 = f(re.search(r"p = __builtin_fmaf\(p, s, ([0-9.e+-]+)f\);\n  float q", body).group(1))
     return [p0, lit("p1"), lit("p2"), lit("p3")], [f(1), lit("q1"), lit("q2"), lit("q3"), lit("q4")], clamp
 
@@ -42,15 +42,18 @@ def _situ_f32(g, u, al, be):
             sc = f(sc * i2)
         return pk, qk, f(C * f(alpha))
 
-    def half(x, pk, qk, c):  # tanh_pq: alpha*tanh(x/alpha) = num/den
-        a = np.minimum(np.maximum(x, -c), c).astype(np.float32)
+    def half(x, pk, qk, c, gate):  # tanh_pq: alpha*tanh(x/alpha) = num/den
+        if gate:  # the gate's clamp is V_MED3_F32, which gives the lower bound for a NaN (the exp keeps it)
+            a = np.where(np.isnan(x), -c, np.clip(x, -c, c)).astype(np.float32)
+        else:  # the up projection's clamp keeps a NaN
+            a = np.minimum(np.maximum(x, -c), c).astype(np.float32)
         s = (a * a).astype(np.float32)
         p = _fma(_fma(_fma(s, pk[3], pk[2]), s, pk[1]), s, pk[0])
         q = _fma(_fma(_fma(_fma(s, qk[4], qk[3]), s, qk[2]), s, qk[1]), s, qk[0])
         return (a * p).astype(np.float32), q
 
-    na, da = half(g, *coef(al))
-    nb, db = half(u, *coef(be))
+    na, da = half(g, *coef(al), True)
+    nb, db = half(u, *coef(be), False)
     d = (da * db).astype(np.float32)
     with np.errstate(over="ignore"):
         e = np.exp(-g.astype(np.float64)).astype(np.float32)
