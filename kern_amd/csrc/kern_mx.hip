@@ -792,59 +792,63 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       const int t = wt * 64 + ts * 16 + c;
-      // h for 4 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
-      float h[4][2];
-#pragma unroll
-      for (int rs = 0; rs < 4; ++rs) {
-        const v4f v = acc[ts][rs];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          h[rs][i] = situ_fast(v[i], v[i + 2], G, U);
-        }
-      }
       const bool ok = t < valid;
       const int64_t p = row0 + t;
-      if (ok && A.dbg) {
+      uint32_t sc = 0;
+      // a 16-row subtile with no live row (a wave-uniform test) needs no SiTU and no codes: its staging rows
+      // are past the tile's live ones, which are never stored, and its sf_c store below is dropped
+      if (wt * 64 + ts * 16 < valid) {
+        // h for 4 subtiles x 2 columns; columns ncol0 + 8*rs + 2*g + {0,1}
+        float h[4][2];
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs) {
+          const v4f v = acc[ts][rs];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) h[rs][i] = situ_fast(v[i], v[i + 2], G, U);
+        }
+        if (ok && A.dbg) {
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              const int n = ncol0 + 8 * rs + 2 * g + i;
+              A.dbg[(p * 3 + 0) * half + n] = acc[ts][rs][i];
+              A.dbg[(p * 3 + 1) * half + n] = acc[ts][rs][i + 2];
+              A.dbg[(p * 3 + 2) * half + n] = h[rs][i];
+            }
+        }
+        // the largest |h| of the lane (IEEE maximum of magnitudes: NaN-propagating, and for other values the
+        // same bits as the largest |bits|), then of the block
+        float fm = __builtin_fabsf(h[0][0]);
 #pragma unroll
         for (int rs = 0; rs < 4; ++rs)
 #pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const int n = ncol0 + 8 * rs + 2 * g + i;
-            A.dbg[(p * 3 + 0) * half + n] = acc[ts][rs][i];
-            A.dbg[(p * 3 + 1) * half + n] = acc[ts][rs][i + 2];
-            A.dbg[(p * 3 + 2) * half + n] = h[rs][i];
+          for (int i = 0; i < 2; ++i) fm = __builtin_elementwise_maximum(fm, __builtin_fabsf(h[rs][i]));
+        sc = mx_scale_code(max_over_rows(__float_as_uint(fm)));
+        uint32_t o[4];
+        mx_code2x4(h, sc, o);
+        if (STAGED) {
+          // wave row r (32 B: the wave's MXFP8 block of the row) at r * 32
+          uint8_t* pc = stg + (16 * ts + c) * 32 + 2 * g;
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs) *reinterpret_cast<uint16_t*>(pc + 8 * rs) = (uint16_t)o[rs];
+        } else if (ok) {
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs)
+            *reinterpret_cast<uint16_t*>(C + p * half + ncol0 + 8 * rs + 2 * g) = (uint16_t)o[rs];
+          if (g == 0) {
+            const int64_t kb4 = ((half >> 5) + 3) >> 2;
+            const int64_t off =
+                512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
+            A.sf_c[off] = (uint8_t)sc;
           }
-      }
-      uint32_t amax = 0;
-#pragma unroll
-      for (int rs = 0; rs < 4; ++rs)
-#pragma unroll
-        for (int i = 0; i < 2; ++i) amax = max(amax, __float_as_uint(h[rs][i]) & 0x7fffffffu);
-      amax = max_over_rows(amax);
-      const uint32_t sc = mx_scale_code(amax);
-      if (STAGED) {
-        // wave row r (32 B: the wave's MXFP8 block of the row) at r * 32
-        uint8_t* pc = stg + (16 * ts + c) * 32 + 2 * g;
-        uint32_t o[4];
-        mx_code2x4(h, sc, o);
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) *reinterpret_cast<uint16_t*>(pc + 8 * rs) = (uint16_t)o[rs];
-      } else if (ok) {
-        uint32_t o[4];
-        mx_code2x4(h, sc, o);
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs)
-          *reinterpret_cast<uint16_t*>(C + p * half + ncol0 + 8 * rs + 2 * g) = (uint16_t)o[rs];
+        }
       }
       if (STAGED) {
         // one byte store per subtile from every lane, the lanes other than g = 0 and the rows past the
         // tile's live ones pointed past the end of sf_c (dropped)
         const int off = sf_base + (t & 31) * 16 + (t >> 5) * 4;
         __builtin_amdgcn_raw_buffer_store_b8((uint8_t)sc, sfr, ok && g == 0 ? off : 0x7fffff00, 0, 0);
-      } else if (ok && g == 0) {
-        const int64_t kb4 = ((half >> 5) + 3) >> 2;
-        const int64_t off = 512 * ((p >> 7) * kb4 + (blk >> 2)) + (p & 31) * 16 + ((p & 127) >> 5) * 4 + (blk & 3);
-        A.sf_c[off] = (uint8_t)sc;
       }
     }
     if (STAGED) {

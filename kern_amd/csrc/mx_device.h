@@ -75,21 +75,13 @@ KERN_DEV uint32_t e4m3_rne(uint32_t bits, int shift) {
   return sign | q;
 }
 
-// floor(log2 |x|) for a finite nonzero f32 given |bits|
-KERN_DEV int floor_log2_abs(uint32_t a) {
-  int E = (int)(a >> 23);
-  if (E > 0) return E - 127;
-  return (31 - __clz(a & 0x7fffffu)) - 149;
-}
-
-// MXFP8 scale code for a block whose largest |bits| is amax (0x7f800000+ means non-finite present)
+// MXFP8 scale code for a block whose largest |bits| is amax: floor(log2 amax) - 8 + 127 clamped to [0, 254] for
+// a finite amax, 255 for a non-finite one (amax_bits >= 0x7f800000). A normal amax has floor(log2) = E - 127 for
+// its exponent field E <= 254, so the code is E - 8; a subnormal or zero amax (E = 0) gives a negative code,
+// clamped to 0, like E <= 8. (The two forms agree on all 2^31 values of |bits|: an exhaustive host check.)
 KERN_DEV uint32_t mx_scale_code(uint32_t amax_bits) {
-  if (amax_bits >= 0x7f800000u) return 255u;
-  if (amax_bits == 0) return 0u;
-  int c = floor_log2_abs(amax_bits) - 8 + 127;
-  c = c < 0 ? 0 : c;
-  c = c > 254 ? 254 : c;
-  return (uint32_t)c;
+  const uint32_t E = amax_bits >> 23;
+  return E >= 255u ? 255u : (E > 8u ? E - 8u : 0u);
 }
 
 // element code of an f32 value in a block with scale code `sc`
