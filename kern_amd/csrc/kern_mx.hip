@@ -700,7 +700,9 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
           v4u d = *reinterpret_cast<const v4u*>(stg + r * 128 + ((k ^ (r & 7)) << 4));
           if (h) d = d.zwxy;
           const int t = wt * 64 + 16 * ts + r;
-          __builtin_amdgcn_raw_buffer_store_b128(d, cr, (t * m + wrow0 + 8 * k) * 2, 0, 0);
+          // FC2's rows are read again only by the finalize's gather: non-temporal stores (config 4: FC2 363 ->
+          // 359 us); the dense GEMM's output keeps the default policy
+          __builtin_amdgcn_raw_buffer_store_b128(d, cr, (t * m + wrow0 + 8 * k) * 2, 0, MODE == MODE_FC2 ? 2 : 0);
         }
       }
     } else {
