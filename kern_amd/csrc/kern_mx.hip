@@ -626,13 +626,16 @@ struct BmmArgs {
 // count of requests sent since, then a barrier), and the compiler's own alias tracking could not tell the
 // ring's slots apart and added waits for every load in flight. M0 holds nothing else in the kernels that use
 // these (no other instruction there reads it).
+// The LDS address of a generic pointer into LDS is its low 32 bits (the shared aperture sits in the high
+// half): taken that way, with no address-space cast, and so no null check on each request.
+KERN_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
 KERN_DEV void dma16(const void* g, void* lds_wave_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_wave_base);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
 }
 // 4 bytes per lane, to `lds_wave_base + 4 * lane`
 KERN_DEV void dma4(const void* g, void* lds_wave_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_wave_base);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
 }
 
@@ -1596,12 +1599,12 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_bf16(const uint8_
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 KERN_DEV void lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, const void* lds_wave_base) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(const lds_void_t*)lds_wave_base;
+  const uint32_t m0v = lds_addr(lds_wave_base);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 KERN_DEV void lds_dma4(__amdgpu_buffer_rsrc_t r, int voff, const void* lds_wave_base) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(const lds_void_t*)lds_wave_base;
+  const uint32_t m0v = lds_addr(lds_wave_base);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
                : "memory", "m0");
 }
