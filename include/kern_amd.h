@@ -276,7 +276,8 @@ int kern_moe_quant_routing(const void* x, void* q, void* sf, int32_t tokens, int
  * a u8 [E][m][k/2] repacked MXFP4, sf_a repacked, b u8 [rows][k] e4m3, sf_b (R128c4 over rows when
  * sf_b_r128c4, else linear [rows][k/32]), c bf16 [rows][m], num_non_exiting, total_padded, cta_batch,
  * cta_limit; launch: m, k, ctas (grid.y, the manifest's E + ceil(tokens*topk/128)), and dbg (NULL or
- * f32 [rows][m] pre-rounding accumulators). m % 256 == 0, k % 512 == 0. */
+ * f32 [rows][m] pre-rounding accumulators). m % 256 == 0, k % 512 == 0; the activations (ctas * 128
+ * rows of k bytes) below 4 GiB, as the kernel addresses them by 32-bit offsets (KERN_ERR_API otherwise). */
 int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c,
                                        const int32_t* num_non_exiting, const int32_t* total_padded,
                                        const int32_t* cta_batch, const int32_t* cta_limit, int32_t m, int32_t k,
@@ -285,7 +286,9 @@ int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a, const void* sf_a, const vo
 /* trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 = moe_fc1 (head.json:25459): a (gated repack), sf_a, b u8 [T][k]
  * e4m3, sf_b linear [T][k/32], c u8 [rows][m/2] e4m3, sf_c u8 R128c4 over rows x (m/2)/32, route_map,
  * alpha f32[E], beta f32[E], num_non_exiting, total_padded, cta_batch, cta_limit; launch m, k, ctas,
- * dbg (NULL or f32 [rows][3][m/2] = gate acc, up acc, SiTU-GLU value). m % 256 == 0, k % 512 == 0. */
+ * dbg (NULL or f32 [rows][3][m/2] = gate acc, up acc, SiTU-GLU value). m % 256 == 0, k % 512 == 0, and
+ * T * k below 2^32 (the kernel addresses the activations by 32-bit offsets; T is not passed, so this one
+ * is the caller's to keep: T < 599,186 tokens at k = 7168). */
 int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c,
                                          void* sf_c, const int32_t* route_map, const float* alpha,
                                          const float* beta, const int32_t* num_non_exiting,
@@ -295,11 +298,11 @@ int kern_trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(const void* a, const void* sf_a, const 
 
 /* Dense e4m3-output mode of the FC1 family (no gate, per-tensor output scale), the prefill GEMM:
  * c[t][n] = e4m3_rne_sat(acc[t][n] * d_scale[0]); a/sf_a repacked [m][k], b u8 [M][k], sf_b linear,
- * c u8 [M][m], d_scale f32[1] on the device; dbg NULL or f32 [M][m]. */
+ * c u8 [M][m], d_scale f32[1] on the device; dbg NULL or f32 [M][m]. M * k below 2^32. */
 int kern_mxfp4_gemm_e4m3(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c,
                          const float* d_scale, int32_t M, int32_t m, int32_t k, float* dbg, void* stream);
 
-/* Dense bf16-output mode of the FC2 family: c bf16 [M][m]. */
+/* Dense bf16-output mode of the FC2 family: c bf16 [M][m]. M * k below 2^32. */
 int kern_mxfp4_gemm_bf16(const void* a, const void* sf_a, const void* b, const void* sf_b, void* c, int32_t M,
                          int32_t m, int32_t k, float* dbg, void* stream);
 

@@ -441,6 +441,10 @@ extern "C" int kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(const void* a_, const void* sf
           m, k, ctas);
   REQUIRE(a_ && sf_a && b && sf_b && c && num_non_exiting && total_padded && cta_batch && cta_limit,
           "trtllm_bmm_bf16_mxe2m1_mxe4m3: null buffer");
+  // the ring addresses the activations by 32-bit byte offsets from the buffer's base
+  REQUIRE((int64_t)ctas * 128 * k < ((int64_t)1 << 32),
+          "trtllm_bmm_bf16_mxe2m1_mxe4m3: activations of ctas * 128 rows x k bytes must stay below 4 GiB (ctas=%d k=%d)",
+          ctas, k);
   if (ctas == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put((void*)c), a.put(num_non_exiting), a.put(total_padded);
@@ -473,6 +477,8 @@ extern "C" int kern_mxfp4_gemm_e4m3(const void* a_, const void* sf_a, const void
   REQUIRE(M >= 0 && m > 0 && m % 256 == 0 && k > 0 && k % 512 == 0,
           "mxfp4_gemm_e4m3: need m %% 256 == 0, k %% 512 == 0 (M=%d m=%d k=%d)", M, m, k);
   REQUIRE(a_ && sf_a && b && sf_b && c && d_scale, "mxfp4_gemm_e4m3: null buffer");
+  REQUIRE((int64_t)M * k < ((int64_t)1 << 32), "mxfp4_gemm_e4m3: activations [M, k] must stay below 4 GiB (M=%d k=%d)",
+          M, k);
   if (M == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(d_scale), a.put(M), a.put(m), a.put(k), a.put(dbg);
@@ -484,6 +490,8 @@ extern "C" int kern_mxfp4_gemm_bf16(const void* a_, const void* sf_a, const void
   REQUIRE(M >= 0 && m > 0 && m % 256 == 0 && k > 0 && k % 512 == 0,
           "mxfp4_gemm_bf16: need m %% 256 == 0, k %% 512 == 0 (M=%d m=%d k=%d)", M, m, k);
   REQUIRE(a_ && sf_a && b && sf_b && c, "mxfp4_gemm_bf16: null buffer");
+  REQUIRE((int64_t)M * k < ((int64_t)1 << 32), "mxfp4_gemm_bf16: activations [M, k] must stay below 4 GiB (M=%d k=%d)",
+          M, k);
   if (M == 0) return KERN_OK;
   Args a;
   a.put(a_), a.put(sf_a), a.put(b), a.put(sf_b), a.put(c), a.put(M), a.put(m), a.put(k), a.put(dbg);

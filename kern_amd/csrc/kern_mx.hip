@@ -638,6 +638,28 @@ KERN_DEV void dma4(const void* g, void* lds_wave_base) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
 }
+// The same requests with a wave-uniform base in an SGPR pair and a per-lane 32-bit byte offset (the
+// instructions' SADDR form): the per-lane address needs no 64-bit add per request, and a k step moves the
+// base once for all of a wave's requests into that buffer.
+KERN_DEV uint64_t uniform_ptr(const void* p) {
+  const uint64_t b = (uint64_t)(uintptr_t)p;
+  // readfirstlane returns an int: each half goes through uint32_t, so the low half is not sign-extended
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  return ((uint64_t)hi << 32) | (uint64_t)lo;
+}
+KERN_DEV void dma16s(const void* base, uint32_t voff, void* lds_wave_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)),
+               "s"(lds)
+               : "memory");
+}
+KERN_DEV void dma4s(const void* base, uint32_t voff, void* lds_wave_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)),
+               "s"(lds)
+               : "memory");
+}
 
 // The LDS ring: four tile stages of each operand, two scale slots of each kind.
 struct BmmLds {
@@ -978,14 +1000,14 @@ KERN_DEV void ring_req_w(const RingTile& T, int KT, int gw, int lane, int kt, ui
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int f = r * 4 + gw;  // fragment (16-row group) 0..15
-    dma16(T.wbase + ((int64_t)f * KT + kt) * 1024 + lane * 16, sW + f * 1024);
+    dma16s(T.wbase + (int64_t)kt * 1024, (uint32_t)(f * KT * 1024 + lane * 16), sW + f * 1024);
   }
 }
 KERN_DEV void ring_req_ws(const RingTile& T, int KG, int gw, int lane, int kg, uint8_t* sSW) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int f = r * 4 + gw;
-    dma4(T.sbase + ((int64_t)f * KG + kg) * 256 + lane * 4, sSW + f * 256);
+    dma4s(T.sbase + (int64_t)kg * 256, (uint32_t)(f * KG * 256 + lane * 4), sSW + f * 256);
   }
 }
 // Activation requests read through per-tile sources: xs[r], this lane's 16 bytes of request r at k-tile 0,
@@ -996,30 +1018,33 @@ KERN_DEV void ring_req_ws(const RingTile& T, int KG, int gw, int lane, int kg, u
 // read a row's four k-tiles in one 16-byte read per group (a k-tile's scale dword holds the row's four
 // 32-wide k blocks). Scale rows: linear [T][K/32], or R128c4 (one 512-byte tile per 128 rows x 4 k blocks).
 struct RingXSrc {
-  const uint8_t* xs[4];
-  const uint8_t* sxs[2];
+  const uint8_t* xb;   // the activations (uniform)
+  const uint8_t* sxb;  // their scales (uniform)
+  uint32_t xs[4];      // byte offsets from xb and sxb (the activation buffers stay below 4 GiB)
+  uint32_t sxs[2];
 };
 KERN_DEV RingXSrc ring_xsrc(const BmmArgs& A, const RingTile& T, int gw, int lane) {
   RingXSrc S;
   const int K = A.k;
+  S.xb = A.b, S.sxb = A.sf_b;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = 32 * r + 8 * gw + (lane >> 3);
-    S.xs[r] = A.b + (int64_t)T.xtok[r] * K + (((lane & 7) ^ ((t >> 1) & 7)) << 4);
+    S.xs[r] = (uint32_t)T.xtok[r] * (uint32_t)K + (((lane & 7) ^ ((t >> 1) & 7)) << 4);
   }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int64_t srow = T.stok[h];
-    S.sxs[h] = A.sf_b_r128c4 ? A.sf_b + 512 * ((srow >> 7) * (int64_t)(K >> 7) + (lane & 3)) + (srow & 31) * 16 +
+    const uint32_t srow = (uint32_t)T.stok[h];
+    S.sxs[h] = A.sf_b_r128c4 ? 512u * ((srow >> 7) * (uint32_t)(K >> 7) + (lane & 3)) + (srow & 31) * 16 +
                                    ((srow & 127) >> 5) * 4
-                             : A.sf_b + srow * (K >> 5) + (lane & 3) * 4;
+                             : srow * (uint32_t)(K >> 5) + (lane & 3) * 4;
   }
   return S;
 }
 template <int NXR>
 KERN_DEV void ring_req_x(const RingXSrc& S, int gw, int kt, uint8_t* sX) {
 #pragma unroll
-  for (int r = 0; r < NXR; ++r) dma16(S.xs[r] + (int64_t)kt * 128, sX + (r * 4 + gw) * 1024);
+  for (int r = 0; r < NXR; ++r) dma16s(S.xb + (int64_t)kt * 128, S.xs[r], sX + (r * 4 + gw) * 1024);
 }
 // k group kg of the scale rows: 4 k-tiles on, 16 bytes (linear) or four 512-byte tiles (R128c4)
 template <int NXR>
@@ -1027,7 +1052,7 @@ KERN_DEV void ring_req_xs(const BmmArgs& A, const RingXSrc& S, int gw, int kg, u
   constexpr int NXS = NXR > 2 ? 2 : 1;
   const int64_t step = A.sf_b_r128c4 ? 2048 : 16;
 #pragma unroll
-  for (int h = 0; h < NXS; ++h) dma4(S.sxs[h] + kg * step, sSX + 256 * (4 * h + gw));
+  for (int h = 0; h < NXS; ++h) dma4s(S.sxb + kg * step, S.sxs[h], sSX + 256 * (4 * h + gw));
 }
 
 // A first tile's first requests (a tile no earlier tile chained to): group 0 the weight scales of k group 0

@@ -87,6 +87,9 @@ def test_kernarg_sizes_from_metadata_match_index(lib):
     assert lib.kern_code_object_param_sizes(img, len(img), b"kern_mx_nope", sizes, 4, ctypes.byref(n)) == 2
 
 
+_NZ = ctypes.c_void_p(16)  # a non-null address that no call here dereferences (the checks fail first)
+
+
 @pytest.mark.parametrize("call,msg", [
     (lambda L: L.kern_moe_quant(None, None, None, 4, 33, None), "K % 32"),
     (lambda L: L.kern_moe_w_shuffle(None, None, 1, 15, 256, 0, None), "rows % 16"),
@@ -100,6 +103,10 @@ def test_kernarg_sizes_from_metadata_match_index(lib):
     (lambda L: L.kern_mxfp4_gemm_bf16(*([None] * 5), -1, 256, 512, None, None), "m % 256"),
     (lambda L: L.kern_moe_routing(*([None] * 8), 4, 2, 0, 513, None), "local_experts <= 512"),
     (lambda L: L.kern_fill_random_u8(None, 16, 1, 0, 0, None), "span"),
+    # the LDS ring addresses activations by 32-bit offsets from the buffer's base: past 4 GiB is refused
+    (lambda L: L.kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(*([_NZ] * 9), 256, 8192, 4200, 1, None, None), "below 4 GiB"),
+    (lambda L: L.kern_mxfp4_gemm_e4m3(*([_NZ] * 6), 1 << 20, 256, 8192, None, None), "below 4 GiB"),
+    (lambda L: L.kern_mxfp4_gemm_bf16(*([_NZ] * 5), 1 << 20, 256, 8192, None, None), "below 4 GiB"),
 ])
 def test_contract_violations_are_api_errors(lib, call, msg):
     rc = call(lib)
