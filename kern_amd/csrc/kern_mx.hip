@@ -213,7 +213,7 @@ KERN_DEV v4f gemv_rows(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr_, __
       }
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
-        const float s = e8m0_to_f32(sl[(i0 + u) * 256]);
+        const float s = fp4_cvt_scale(sl[(i0 + u) * 256]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           // A: 8 fp4 of this lane's row, k = 32*grp + 8*j .. +8 of the tile (dword j of the lane's slot)
@@ -331,7 +331,7 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16_rg(
       const uint16_t* xk = xl + g * M * 512;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const float s = e8m0_to_f32((sc >> (8 * u)) & 0xffu);
+        const float s = fp4_cvt_scale((sc >> (8 * u)) & 0xffu);
         if (xlive) {
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) xb[jj] = *reinterpret_cast<const v4u*>(xk + u * 128 + jj * 8);
@@ -425,7 +425,7 @@ KERN_DEV void gemv_rows_fixed(const uint16_t* __restrict__ x, const uint8_t* __r
     const v4u wv = buf[i % D];
     const int kt = kt0 + i;
     const uint32_t dw = ((ph + i) >> 2) == (i >> 2) ? sdw[i >> 2] : sdw[(i >> 2) + 1];
-    const float s = e8m0_to_f32((dw >> (8 * (kt & 3))) & 255u);
+    const float s = fp4_cvt_scale((dw >> (8 * (kt & 3))) & 255u);
     if (xlive) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) xb[jj] = *reinterpret_cast<const v4u*>(xl + i * 128 + jj * 8);
@@ -528,7 +528,7 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
   for (int i = 0; i < TOT; ++i) {
     const int g = i / KTW, j = i % KTW, kt = kt0 + j;
     const v4u wv = buf[i % D];
-    const float s = e8m0_to_f32((sdw[g][(kt >> 2) - kgA] >> (8 * (kt & 3))) & 0xffu);
+    const float s = fp4_cvt_scale((sdw[g][(kt >> 2) - kgA] >> (8 * (kt & 3))) & 0xffu);
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const uint32_t wd = wv[jj];

@@ -225,6 +225,12 @@ KERN_DEV float situ_fast(float g, float u, const SituCoef& G, const SituCoef& U)
   return (na * nb) * __builtin_amdgcn_rcpf(__builtin_fmaf(d, __expf(-g), d));
 }
 
+// The scale operand of V_CVT_SCALEF32_PK_BF16_FP4 for e8m0 code `code`: the instruction reads only the
+// operand's exponent field as an e8m0 code, so the bare field (code << 23) converts exactly as
+// e8m0_to_f32(code) does, codes 0 and 255 included (all 256 codes x 256 byte patterns x 4 selects compared
+// on the device).
+KERN_DEV float fp4_cvt_scale(uint32_t code) { return __uint_as_float(code << 23); }
+
 // f32 value 2^(code-127) (code 0 is the subnormal 2^-127, 255 is NaN)
 KERN_DEV float e8m0_to_f32(uint32_t code) {
   const uint32_t b = code == 0u ? 0x00400000u : (code == 255u ? 0x7fc00000u : code << 23);  // selects, no branches
