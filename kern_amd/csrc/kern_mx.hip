@@ -631,12 +631,12 @@ struct BmmArgs {
 KERN_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
 KERN_DEV void dma16(const void* g, void* lds_wave_base) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 // 4 bytes per lane, to `lds_wave_base + 4 * lane`
 KERN_DEV void dma4(const void* g, void* lds_wave_base) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 // The same requests with a wave-uniform base in an SGPR pair and a per-lane 32-bit byte offset (the
 // instructions' SADDR form): the per-lane address needs no 64-bit add per request, and a k step moves the
@@ -652,13 +652,13 @@ KERN_DEV void dma16s(const void* base, uint32_t voff, void* lds_wave_base) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)),
                "s"(lds)
-               : "memory");
+               : "memory", "m0");
 }
 KERN_DEV void dma4s(const void* base, uint32_t voff, void* lds_wave_base) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)),
                "s"(lds)
-               : "memory");
+               : "memory", "m0");
 }
 
 // The LDS ring: four tile stages of each operand, two scale slots of each kind.
@@ -1628,6 +1628,13 @@ KERN_DEV void lds_dma16(__amdgpu_buffer_rsrc_t r, int voff, const void* lds_wave
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
                : "memory", "m0");
 }
+// the same with the k step's byte offset in soffset (an SGPR, wave-uniform): no per-lane add per request
+KERN_DEV void lds_dma16so(__amdgpu_buffer_rsrc_t r, int voff, int soff, const void* lds_wave_base) {
+  const uint32_t m0v = lds_addr(lds_wave_base);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0v), "v"(voff), "s"(r),
+               "s"(soff)
+               : "memory", "m0");
+}
 KERN_DEV void lds_dma4(__amdgpu_buffer_rsrc_t r, int voff, const void* lds_wave_base) {
   const uint32_t m0v = lds_addr(lds_wave_base);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
@@ -1688,12 +1695,22 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8
     // no masks. The offsets pass through an empty asm so that no copy of them is kept per step.
     int oa[2] = {offa[0], offa[1]}, ow[4] = {offw[0], offw[1], offw[2], offw[3]};
     asm volatile("" : "+v"(oa[0]), "+v"(oa[1]), "+v"(ow[0]), "+v"(ow[1]), "+v"(ow[2]), "+v"(ow[3]));
-    const bool in_k = kt * 128 + jb < K;  // 0xFFFFFFF0 lies past any operand (they are below 2 GiB)
+    if (kt * 128 + 128 <= K) {
+      // a whole k-tile (wave-uniform test): the k step's offset goes in soffset
+      int so = __builtin_amdgcn_readfirstlane(kt * 128);
+      asm volatile("" : "+s"(so));
 #pragma unroll
-    for (int r = 0; r < 2; ++r) lds_dma16(ra, in_k ? oa[r] + kt * 128 : (int)0xFFFFFFF0u, stg + (r * 8 + wave) * 1024);
+      for (int r = 0; r < 2; ++r) lds_dma16so(ra, oa[r], so, stg + (r * 8 + wave) * 1024);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      lds_dma16(rw, in_k ? ow[r] + kt * 128 : (int)0xFFFFFFF0u, stg + G8_XT + (r * 8 + wave) * 1024);
+      for (int r = 0; r < 4; ++r) lds_dma16so(rw, ow[r], so, stg + G8_XT + (r * 8 + wave) * 1024);
+    } else {
+      const bool in_k = kt * 128 + jb < K;  // 0xFFFFFFF0 lies past any operand (they are below 2 GiB)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) lds_dma16(ra, in_k ? oa[r] + kt * 128 : (int)0xFFFFFFF0u, stg + (r * 8 + wave) * 1024);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        lds_dma16(rw, in_k ? ow[r] + kt * 128 : (int)0xFFFFFFF0u, stg + G8_XT + (r * 8 + wave) * 1024);
+    }
     lds_dma4(rs, soff + kt * 512, stg + G8_XT + G8_WT + wave * 256);
   };
 

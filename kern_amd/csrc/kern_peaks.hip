@@ -134,6 +134,34 @@ extern "C" __global__ __launch_bounds__(256) void kern_peak_stream(const v4u* __
 
 extern "C" __global__ void kern_peak_empty(int* out) { (void)out; }
 
+// The GEMVs' fp4 -> bf16 conversion scale (fp4_cvt_scale: the bare e8m0 exponent field) against the f32 value
+// e8m0_to_f32 of the same code: thread (code = blockIdx.x, byte = threadIdx.x) converts a dword holding the
+// byte in each position under both, all four byte selects; mismatches are counted in out[0], the last one's
+// (code << 8 | byte) in out[1]. Grid 256, block 256.
+typedef __bf16 v2bf16_t __attribute__((ext_vector_type(2)));
+extern "C" __global__ __launch_bounds__(256) void kern_probe_fp4_scale(uint32_t* out) {
+  const uint32_t code = blockIdx.x, b = threadIdx.x;
+  const uint32_t w = b | (((b * 0x9E3779B9u) >> 8) & 0xffffff00u);
+  const float s_val = e8m0_to_f32(code), s_fld = fp4_cvt_scale(code);
+  uint32_t bad = 0;
+#pragma unroll
+  for (int sel = 0; sel < 4; ++sel) {
+    const uint32_t ws = sel == 0 ? w : (sel == 1 ? ((w << 8) | b) : (sel == 2 ? ((w << 16) | (b << 8) | b) : (w << 24) | (b * 0x010101u)));
+    const v2bf16_t x0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_val, 0), y0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_fld, 0);
+    const v2bf16_t x1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_val, 1), y1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_fld, 1);
+    const v2bf16_t x2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_val, 2), y2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_fld, 2);
+    const v2bf16_t x3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_val, 3), y3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws, s_fld, 3);
+    bad += (__builtin_bit_cast(uint32_t, x0) != __builtin_bit_cast(uint32_t, y0)) +
+           (__builtin_bit_cast(uint32_t, x1) != __builtin_bit_cast(uint32_t, y1)) +
+           (__builtin_bit_cast(uint32_t, x2) != __builtin_bit_cast(uint32_t, y2)) +
+           (__builtin_bit_cast(uint32_t, x3) != __builtin_bit_cast(uint32_t, y3));
+  }
+  if (bad) {
+    atomicAdd(out, bad);
+    out[1] = (code << 8) | b;
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256) void kern_probe_bf16_cvt(uint32_t lo, uint32_t n, uint32_t* out) {
   uint32_t bad = 0, which = 0;
   const uint64_t stride = (uint64_t)gridDim.x * 256u;
