@@ -180,11 +180,14 @@ def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
 # --------------------------------------------------------------------------------------- routing
 
 # uniform ids; every token on the same k experts (slots of 128 rows, several per expert); the 512-expert
-# maximum; a segment per wave of several 64-index rounds (T*k = 65536)
+# maximum; a segment per wave of several 64-index rounds (T*k = 65536); decode sizes: 64 indices (one wave's
+# round), with non-local experts, with every token on the same experts, and 65 (a second round)
 @pytest.mark.parametrize("T,E,k,start,local,skew", [(512, 256, 8, 0, 256, 0), (37, 16, 4, 4, 8, 0),
                                                     (1, 8, 2, 0, 8, 0), (300, 224, 16, 56, 56, 0),
                                                     (2048, 64, 6, 0, 64, 0), (1000, 64, 4, 0, 64, 1),
-                                                    (100, 512, 8, 0, 512, 0), (8192, 256, 8, 0, 256, 0)])
+                                                    (100, 512, 8, 0, 512, 0), (8192, 256, 8, 0, 256, 0),
+                                                    (8, 256, 8, 0, 256, 0), (4, 224, 16, 56, 56, 0),
+                                                    (8, 64, 8, 0, 64, 1), (13, 16, 5, 2, 8, 0)])
 def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
     ids = wl.topk_ids(T * 31 + E, T, E, k)
     if skew:
