@@ -2086,6 +2086,11 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize_rms(
   (void)T;
   const int t = blockIdx.x, tid = threadIdx.x, chunks = H >> 3;
   constexpr int Q = 4;  // chunks per thread kept in registers between the passes (H <= 8192)
+  // gamma's chunks first: their loads overlap the routed rows' instead of following the reduction
+  v4u gm[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    gm[q] = tid + 256 * q < chunks ? *reinterpret_cast<const v4u*>(gamma + (tid + 256 * q) * 8) : (v4u){0, 0, 0, 0};
   float y[Q][8];
   float ss = 0.f;
   moe_combine_chunks<Q>(fc2_out, exp2perm, topk_w, t, H, topk, tid, chunks, y);
@@ -2106,10 +2111,9 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize_rms(
   for (int q = 0; q < Q; ++q) {
     const int c = tid + 256 * q;
     if (c < chunks) {
-      const v4u gm = *reinterpret_cast<const v4u*>(gamma + c * 8);
       float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = y[q][e] * r * bf16_bits_to_f32((gm[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+      for (int e = 0; e < 8; ++e) v[e] = y[q][e] * r * bf16_bits_to_f32((gm[q][e >> 1] >> (16 * (e & 1))) & 0xffffu);
       *reinterpret_cast<v4u*>(out + (int64_t)t * H + c * 8) = bf16x8(v);
     }
   }
