@@ -1336,21 +1336,28 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
   const int K = A.k, KT = K >> 7, KG = K >> 9, m = A.m;
   const int c = lane & 15, g = lane >> 4;
   const int rg0 = (nx * BN) >> 4;
-  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)(rg0 + 4 * hw) * KT) * 1024 + lane * 16;
-  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)(rg0 + 4 * hw) * KG) * 256 + lane * 4;
+  // wave-uniform bases with 32-bit per-lane offsets (the activations stay below 4 GiB): each load is a
+  // uniform base plus a k step in SGPRs and one VGPR offset, with no 64-bit address arithmetic per lane
+  const uint8_t* wbase = A.a + (int64_t)expert * m * (K >> 1) + ((int64_t)(rg0 + 4 * hw) * KT) * 1024;
+  const uint8_t* sbase = A.sf_a + (int64_t)expert * m * (K >> 5) + ((int64_t)(rg0 + 4 * hw) * KG) * 256;
+  const uint32_t wl = (uint32_t)lane * 16u, sl = (uint32_t)lane * 4u;
+  // buffer resources over the tile's weights and scales and over the activations, with the full 4 GiB
+  // range (every offset stays inside its buffer); the k step goes in the instruction's scalar offset
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)wbase, (short)0, -1, 0x00020000);
+  const __amdgpu_buffer_rsrc_t swr = __builtin_amdgcn_make_buffer_rsrc((void*)sbase, (short)0, -1, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)A.b, (short)0, -1, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sxr = __builtin_amdgcn_make_buffer_rsrc((void*)A.sf_b, (short)0, -1, 0x00020000);
   // this lane's activation row in each 16-row subtile: rows past the slot read the slot's first row and
   // are never stored
-  const uint8_t* xp[NTS];
-  const uint8_t* sxp[NTS];
+  uint32_t xo[NTS > 0 ? NTS : 1], sxo[NTS > 0 ? NTS : 1];
   const int sx_kstep = A.sf_b_r128c4 ? 512 : 4;
 #pragma unroll
   for (int ts = 0; ts < NTS; ++ts) {
     const int t = ts * 16 + c < valid ? ts * 16 + c : 0;
-    const int64_t xrow = MODE == MODE_FC1 ? (int64_t)A.route_map[row0 + t] : (int64_t)(row0 + t);
-    xp[ts] = A.b + xrow * K + 16 * g;
-    sxp[ts] = A.sf_b_r128c4
-                  ? A.sf_b + 512 * ((xrow >> 7) * (int64_t)(K >> 7)) + (xrow & 31) * 16 + ((xrow & 127) >> 5) * 4 + g
-                  : A.sf_b + xrow * (K >> 5) + g;
+    const uint32_t xrow = MODE == MODE_FC1 ? (uint32_t)A.route_map[row0 + t] : (uint32_t)(row0 + t);
+    xo[ts] = xrow * (uint32_t)K + 16u * g;
+    sxo[ts] = A.sf_b_r128c4 ? 512u * ((xrow >> 7) * (uint32_t)(K >> 7)) + (xrow & 31) * 16 + ((xrow & 127) >> 5) * 4 + g
+                            : xrow * (uint32_t)(K >> 5) + g;
   }
   v4f acc[4][4];
 #pragma unroll
@@ -1368,17 +1375,17 @@ KERN_DEV void skinny_tile(const BmmArgs& A, int nx, int expert, int row0, int va
     if (st == 0) {
 #pragma unroll
       for (int f = 0; f < 4; ++f)
-        swq[sg][f] = *reinterpret_cast<const uint32_t*>(sbase + ((int64_t)f * KG + (kt >> 2)) * 256);
+        swq[sg][f] = __builtin_amdgcn_raw_buffer_load_b32(swr, f * KG * 256 + sl, (kt >> 2) * 256, 0);
     }
 #pragma unroll
     for (int f = 0; f < 4; ++f)  // weights are read once: non-temporal
-      wq[st][f] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wbase + ((int64_t)f * KT + kt) * 1024));
+      wq[st][f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, f * KT * 1024 + wl, kt * 1024, 2));
 #pragma unroll
     for (int ts = 0; ts < NTS; ++ts) {
       // the B operand's two 16-byte chunks of the k-tile, g and g + 4 (the layout the MFMA reads)
-      xq[st][ts][0] = *reinterpret_cast<const v4i*>(xp[ts] + (int64_t)kt * 128);
-      xq[st][ts][1] = *reinterpret_cast<const v4i*>(xp[ts] + (int64_t)kt * 128 + 64);
-      sxq[st][ts] = sxp[ts][(int64_t)kt * sx_kstep];
+      xq[st][ts][0] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[ts], kt * 128, 0));
+      xq[st][ts][1] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[ts] + 64, kt * 128, 0));
+      sxq[st][ts] = __builtin_amdgcn_raw_buffer_load_b8(sxr, sxo[ts], kt * sx_kstep, 0);
     }
   };
   auto compute = [&](auto Sc) {
