@@ -507,7 +507,9 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
   // K = 512 * NKT with an unrolled instance for NKT: each of the four waves owns NKT consecutive k-tiles
   const char* fixed = kg == 2 ? "kern_mx_gemv_bf16_r2" : kg == 4 ? "kern_mx_gemv_bf16_r4" : kg == 8 ? "kern_mx_gemv_bf16_r8"
                       : kg == 14 ? "kern_mx_gemv_bf16_r14" : kg == 16 ? "kern_mx_gemv_bf16_r16" : nullptr;
-  if (M <= 2 && fixed) {
+  // M = 3 too at the long K of configs 2 and 5 (K = 7168: 13.8 us against 14.4 for the persistent kernel at
+  // N = 18432; from M = 4 on the persistent kernel is faster, 14.5 against 16.5 us)
+  if ((M <= 2 || (M == 3 && kg >= 14)) && fixed) {
     // one workgroup per 16-row group; each wave's x slice (M * NKT * 256 B) in its own LDS region
     Args a;
     a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K);

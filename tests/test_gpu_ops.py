@@ -89,7 +89,8 @@ def test_repack_bitexact(ops, oracle, gated):
 # --------------------------------------------------------------------------------------- decode GEMV
 
 # kern_mxfp4_gemv_bf16 picks a kernel by shape; the cases cover each:
-#   M <= 2, K = 512 * {2, 4, 8, 14, 16} -> kern_mx_gemv_bf16_r{2,4,8,14,16} (unrolled);
+#   M <= 2, K = 512 * {2, 4, 8, 14, 16} -> kern_mx_gemv_bf16_r{2,4,8,14,16} (unrolled), and M = 3 at
+#   K = 7168 and 8192;
 #   M <= 2, other K -> kern_mx_gemv_bf16_rg (k groups split four ways: KG = 1, 3, 7, 32);
 #   M > 2, K = 1024 * {1, 2, 4, 7, 8} -> kern_mx_gemv_bf16_p{1,2,4,7,8} (half-group shares of 1 and 9,
 #   a ragged last workgroup at N = 18448);
@@ -107,7 +108,8 @@ def test_repack_bitexact(ops, oracle, gated):
                                          (2, 112, 8192, 118, 136), (1, 9216, 7168, 122, 132),
                                          (1, 16384, 2048, 122, 132), (2, 16384, 4096, 122, 132),
                                          (1, 16384, 8192, 122, 132), (4, 512, 512, 122, 132),
-                                         (16, 48, 512, 118, 136), (3, 64, 1536, 122, 132)])
+                                         (16, 48, 512, 118, 136), (3, 64, 1536, 122, 132),
+                                         (3, 18432, 7168, 122, 132), (3, 7168, 8192, 122, 132)])
 def test_gemv_w4a16(ops, oracle, M, N, K, lo, hi):
     x = wl.activations_bf16(100 + M, M, K)
     w, sf = wl.mxfp4_weights(200 + M, 1, N, K, lo, hi)
