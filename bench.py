@@ -70,7 +70,7 @@ DN, DK = 18432, 7168
 
 def gemv_kernel(M):
     """The kernel kern_mxfp4_gemv_bf16 launches for config 2 (K = 7168) at M tokens."""
-    return "kern_mx_gemv_bf16_r14" if M <= 2 else "kern_mx_gemv_bf16_p7"
+    return "kern_mx_gemv_bf16_r14" if M <= 3 else "kern_mx_gemv_bf16_p7"
 
 # config 4 (MoE grouped), BASELINE.json configs[3]
 MT, ME, MTOP, MH, MI = 512, 256, 8, 7168, 2048

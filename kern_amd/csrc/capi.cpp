@@ -507,9 +507,14 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
   // K = 512 * NKT with an unrolled instance for NKT: each of the four waves owns NKT consecutive k-tiles
   const char* fixed = kg == 2 ? "kern_mx_gemv_bf16_r2" : kg == 4 ? "kern_mx_gemv_bf16_r4" : kg == 8 ? "kern_mx_gemv_bf16_r8"
                       : kg == 14 ? "kern_mx_gemv_bf16_r14" : kg == 16 ? "kern_mx_gemv_bf16_r16" : nullptr;
-  // M = 3 too at the long K of configs 2 and 5 (K = 7168: 13.8 us against 14.4 for the persistent kernel at
-  // N = 18432; from M = 4 on the persistent kernel is faster, 14.5 against 16.5 us)
-  if ((M <= 2 || (M == 3 && kg >= 14)) && fixed) {
+  // Also taken at M = 3, and at any M while N <= 8192, as long as the x slices fit in 144 KiB of LDS.
+  // Each workgroup reads all of x, so the persistent kernel's x reuse wins from M = 4 on at large N
+  // (K = 7168, N = 9216: 9.8 against 10.1 us; N = 18432: 13.2 against 16.3). At M = 3 the two are within
+  // 5% either way (N = 9216: 9.2 against 9.7 us; N = 18432: 13.6 against 13.2). At N <= 8192 the
+  // persistent workgroups own four or fewer half groups, and the row-group kernel stays ahead:
+  //   N = 7168, K = 8192, M = 8: 10.0 against 10.5 us;
+  //   N = 4096, K = 4096, M = 16: 5.3 against 7.5 us.
+  if (fixed && 2 * M * K <= 144 * 1024 && (M <= 3 || N <= 8192)) {
     // one workgroup per 16-row group; each wave's x slice (M * NKT * 256 B) in its own LDS region
     Args a;
     a.put(x), a.put(w), a.put(w_sf), a.put(y), a.put(M), a.put(N), a.put(K);
@@ -528,7 +533,8 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
                                             "kern_mx_gemv_bf16_p8"};
   if (K % 1024 == 0 && K / 1024 <= 8 && persistent[K / 1024]) {
     // about 256 workgroups of 8 waves, each owning hb <= 9 half groups of 8 rows (at most five 16-row
-    // groups); wave w owns k-tiles [w*K/1024, (w+1)*K/1024) and holds their x in registers
+    // groups); wave w owns k-tiles [w*K/1024, (w+1)*K/1024) and holds their x in registers, one k-tile
+    // at a time
     const int32_t H = N / 8;
     const int32_t hb = std::min<int32_t>(9, (H + 255) / 256);
     Args a;

@@ -89,11 +89,11 @@ def test_repack_bitexact(ops, oracle, gated):
 # --------------------------------------------------------------------------------------- decode GEMV
 
 # kern_mxfp4_gemv_bf16 picks a kernel by shape; the cases cover each:
-#   M <= 2, K = 512 * {2, 4, 8, 14, 16} -> kern_mx_gemv_bf16_r{2,4,8,14,16} (unrolled), and M = 3 at
-#   K = 7168 and 8192;
+#   K = 512 * {2, 4, 8, 14, 16} with 2*M*K <= 144 KiB and M <= 3 or N <= 8192 ->
+#   kern_mx_gemv_bf16_r{2,4,8,14,16} (unrolled; M = 8 at N = 512, 16 at N = 4096, 9 at the LDS bound);
 #   M <= 2, other K -> kern_mx_gemv_bf16_rg (k groups split four ways: KG = 1, 3, 7, 32);
-#   M > 2, K = 1024 * {1, 2, 4, 7, 8} -> kern_mx_gemv_bf16_p{1,2,4,7,8} (half-group shares of 1 and 9,
-#   a ragged last workgroup at N = 18448);
+#   otherwise K = 1024 * {1, 2, 4, 7, 8} -> kern_mx_gemv_bf16_p{1,2,4,7,8} (half-group shares of 1, 4,
+#   5, 6, 8 and 9, ragged last workgroups at N = 8336, 9216 and 18448, M = 10 just past the LDS bound);
 #   anything else -> kern_mx_gemv_bf16 (K = 1536, 3072).
 @pytest.mark.parametrize("M,N,K,lo,hi", [(8, 512, 1024, 124, 130), (1, 18432, 7168, 122, 132),
                                          (4, 18432, 7168, 122, 132), (16, 18432, 7168, 122, 132),
@@ -109,7 +109,11 @@ def test_repack_bitexact(ops, oracle, gated):
                                          (1, 16384, 2048, 122, 132), (2, 16384, 4096, 122, 132),
                                          (1, 16384, 8192, 122, 132), (4, 512, 512, 122, 132),
                                          (16, 48, 512, 118, 136), (3, 64, 1536, 122, 132),
-                                         (3, 18432, 7168, 122, 132), (3, 7168, 8192, 122, 132)])
+                                         (3, 18432, 7168, 122, 132), (3, 7168, 8192, 122, 132),
+                                         (16, 4096, 4096, 122, 132), (9, 7168, 8192, 122, 132),
+                                         (10, 7168, 8192, 122, 132), (4, 8336, 1024, 122, 132),
+                                         (6, 16384, 2048, 122, 132), (5, 12288, 4096, 122, 132),
+                                         (4, 9216, 7168, 122, 132)])
 def test_gemv_w4a16(ops, oracle, M, N, K, lo, hi):
     x = wl.activations_bf16(100 + M, M, K)
     w, sf = wl.mxfp4_weights(200 + M, 1, N, K, lo, hi)
