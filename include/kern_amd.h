@@ -308,7 +308,7 @@ int kern_mxfp4_gemm_bf16(const void* a, const void* sf_a, const void* b, const v
 
 /* mxfp4_gemv_bf16 (new op; the W4A16 decode, no reference counterpart): in bf16 x[M][K], in u8 w
  * repacked [N][K/2], in u8 w_sf repacked, out bf16 y[M][N], i32 M (1..16); launch N, K.
- * N % 16 == 0, K % 512 == 0. */
+ * N % 16 == 0, K % 512 == 0, K <= 16384. */
 int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_sf, void* y, int32_t M, int32_t N, int32_t K,
                          void* stream);
 
