@@ -582,6 +582,134 @@ GEMV_PERSISTENT(7)
 GEMV_PERSISTENT(8)
 #undef GEMV_PERSISTENT
 
+// ------------------------------------- dense MXFP4 x MXFP8 -> bf16 at M <= 32 tokens: the persistent walk
+// The tiled GEMM gives a small batch one workgroup per 256 weight rows (36 at N = 9216). This kernel
+// (up to four 16-token groups; the C ABI sends it at most two) walks the weights as gemv_persistent
+// does (about 256 workgroups of 8 waves, hb <= 9 half groups each, wave w owning k-tiles
+// [w*KTW, (w+1)*KTW) of K = 1024*KTW,
+// k-tile by k-tile across the row groups, fragments six ahead) and multiplies them in their fp4 form on the
+// block-scaled MFMA against the MXFP8 activations of four 16-token groups, fetched one k-tile ahead into
+// registers: lane (c, q) of group tg holds token 16*tg + c's bytes [16q, 16q + 16) and [64 + 16q, +16) of the
+// k-tile (the 8-bit operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4) and its k block q's scale
+// byte; absent tokens read zeros. Both scale operands arrive shifted to byte 0 (OPSEL 0). The eight partial
+// sums meet in LDS one token group at a time; dbg (if not null) receives the f32 sums the bf16 values round.
+template <int KTW>
+KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,
+                               const uint8_t* __restrict__ xq, const uint8_t* __restrict__ xsf,
+                               uint16_t* __restrict__ y, float* __restrict__ dbg, int M, int N, int K, int hb) {
+  constexpr int NG = 5, D = 6, TOT = NG * KTW, TG = 4;
+  __shared__ v4f red[8][NG][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KT = K >> 7, KG = K >> 9, KB = K >> 5;
+  const int H = N >> 3;
+  const int h0 = blockIdx.x * hb, h1 = min(h0 + hb, H);
+  const int g0 = h0 >> 1, ng = ((h1 + 1) >> 1) - g0;  // row groups touched: [g0, g0 + ng), ng <= NG
+  const int c = lane & 15, q = lane >> 4, r = lane & 15;
+  const int kt0 = wave * KTW, kgA = kt0 >> 2;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, M * K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xsr = __builtin_amdgcn_make_buffer_rsrc((void*)xsf, (short)0, M * KB, 0x00020000);
+  int xo[TG], so[TG];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) {
+    const int t = 16 * tg + c;
+    xo[tg] = t < M ? t * K + 128 * kt0 + 16 * q : 0x40000000;
+    so[tg] = t < M ? t * KB + 4 * kt0 : 0x40000000;
+  }
+  v4u xa[KTW][TG], xb[KTW][TG];  // live one k-tile at a time
+  uint32_t xs[KTW][TG];
+  auto load_x = [&](int j) {
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) {
+      xa[j][tg] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[tg] + 128 * j, 0, 0);
+      xb[j][tg] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[tg] + 128 * j + 64, 0, 0);
+      xs[j][tg] = __builtin_amdgcn_raw_buffer_load_b32(xsr, so[tg] + 4 * j, 0, 0);
+    }
+  };
+  load_x(0);
+  // weight-scale dwords of k groups kgA .. kgA + 2 (KTW <= 8 consecutive k-tiles span at most three groups)
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(wsf + (int64_t)g0 * KG * 256), (short)0, ng * KG * 256, 0x00020000);
+  constexpr int NS = (KTW + 6) / 4;
+  uint32_t sdw[NG][NS];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const int kg = kgA + t;
+      sdw[g][t] = __builtin_amdgcn_raw_buffer_load_b32(
+          sr, (g < ng && kg < KG) ? (g * KG + kg) * 256 + lane * 4 : 0x40000000, 0, 2);
+    }
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + (int64_t)g0 * KT * 1024), (short)0, ng * KT * 1024, 0x00020000);
+  // item i = j*NG + g is fragment (g0 + g, kt0 + j); rows outside the owned half groups read zeros
+  auto woff = [&](int i) -> int {
+    const int g = i % NG, half = (g0 + g) * 2 + (r >> 3);
+    return (g < ng && half >= h0 && half < h1) ? (g * KT + kt0 + i / NG) * 1024 + lane * 16 : 0x40000000;
+  };
+  v4u buf[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    if (i < TOT) buf[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff(i), 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  v4f acc[NG][TG] = {};
+#pragma unroll
+  for (int i = 0; i < TOT; ++i) {
+    const int g = i % NG, j = i / NG, kt = kt0 + j;
+    if (g == 0 && j + 1 < KTW) load_x(j + 1);
+    const v4u wv = buf[i % D];
+    if (g < ng) {
+      const int sw = (int)(sdw[g][(kt >> 2) - kgA] >> (8 * (kt & 3)));
+      const v8i a = {(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3], 0, 0, 0, 0};
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg) {
+        if (16 * tg >= M) break;  // token groups with no token (uniform)
+        const v4u lo = xa[j][tg], hi = xb[j][tg];
+        const v8i b = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        const int sx = (int)(xs[j][tg] >> (8 * q));
+        acc[g][tg] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[g][tg], 4, 0, 0, sw, 0, sx);
+      }
+    }
+    if (i + D < TOT) buf[i % D] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff(i + D), 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg) {
+    if (16 * tg >= M) break;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) red[wave][g][lane] = acc[g][tg];
+    __syncthreads();
+    for (int g = wave; g < ng; g += 8) {
+      v4f s = red[0][g][lane];
+#pragma unroll
+      for (int v = 1; v < 8; ++v) s += red[v][g][lane];
+      const int half = (g0 + g) * 2 + (q >> 1), t = 16 * tg + c;
+      if (t < M && half >= h0 && half < h1) {
+        const int64_t o = (int64_t)t * N + (g0 + g) * 16 + q * 4;
+        const uint32_t lo = f32_to_bf16_bits(s[0]) | (f32_to_bf16_bits(s[1]) << 16);
+        const uint32_t hi = f32_to_bf16_bits(s[2]) | (f32_to_bf16_bits(s[3]) << 16);
+        *reinterpret_cast<uint2*>(y + o) = make_uint2(lo, hi);
+        if (dbg) *reinterpret_cast<v4f*>(dbg + o) = s;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+#define GEMM_SKINNY(KTW)                                                                                       \
+  extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_bf16_s##KTW(                                   \
+      const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf, const uint8_t* __restrict__ xq,          \
+      const uint8_t* __restrict__ xsf, uint16_t* __restrict__ y, float* __restrict__ dbg, int M, int N, int K, \
+      int hb) {                                                                                                \
+    gemm_skinny_bf16<KTW>(w, wsf, xq, xsf, y, dbg, M, N, K, hb);                                               \
+  }
+GEMM_SKINNY(1)
+GEMM_SKINNY(2)
+GEMM_SKINNY(4)
+GEMM_SKINNY(7)
+GEMM_SKINNY(8)
+#undef GEMM_SKINNY
+
 // ====================================================================================== block-scaled GEMM
 // One workgroup computes a 128-row (token/slot) x 256-row (weight) tile with 8 waves (two per SIMD) in a
 // 2x4 grid; each wave owns 64 x 64 = 4 x 4 tiles of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (A = fp4 weights,
