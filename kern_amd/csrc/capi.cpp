@@ -549,7 +549,7 @@ extern "C" int kern_mxfp4_gemv_bf16(const void* x, const void* w, const void* w_
   if (K % 1024 == 0 && K / 1024 <= 8 && persistent[K / 1024]) {
     // about 256 workgroups of 8 waves, each owning hb <= 9 half groups of 8 rows (at most five 16-row
     // groups); wave w owns k-tiles [w*K/1024, (w+1)*K/1024) and holds their x in registers, one k-tile
-    // at a time
+    // at a time, passed through 4 KiB of LDS of its own
     const int32_t H = N / 8;
     const int32_t hb = std::min<int32_t>(9, (H + 255) / 256);
     Args a;

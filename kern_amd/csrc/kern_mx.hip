@@ -478,12 +478,17 @@ GEMV_ROWS_FIXED(16)
 // is read once per workgroup instead of once per row group (59 MB of L2 reads at M = 16 against 264 MB)
 // and only one k-tile of x is held: the next k-tile's x is requested as a k-tile starts (fetching all
 // of x up front stalls the weight stream behind it: 17.2 against 15.3 us at M = 16, N = 18432).
+// x is requested row-contiguous (16 lanes a 256-byte row) and passes through 4 KiB of LDS of the wave's
+// own, written as loaded and read back in the MFMA's operand pieces: requested straight in those pieces,
+// each request gathered 16 rows' 16-byte pieces at a 64-byte stride (M = 16: 15.4 against 14.6-15.0 us
+// at N = 18432, 12.5 against 10.5 at N = 7168, K = 8192).
 // Fragments stream six ahead. The eight partial sums meet in LDS.
 template <int KTW>
 KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
                               const uint8_t* __restrict__ wsf, uint16_t* __restrict__ y, int M, int N, int K, int hb) {
   constexpr int NG = 5, D = 6, TOT = NG * KTW;
   __shared__ v4f red[8][NG][64];
+  __shared__ __attribute__((aligned(16))) uint8_t xst[8][4096];  // per wave, one k-tile of x (16 rows x 256 B)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KT = K >> 7, KG = K >> 9;
   const int H = N >> 3;
@@ -493,10 +498,20 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
   const int kt0 = wave * KTW, kgA = kt0 >> 2;
   // x: lane (c, kq) holds x[c][128*kt + 32*kq .. +32] for each of its k-tiles (absent tokens: zeros)
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, 0x00020000);
-  const int xoff = c < M ? (c * K + 128 * kt0 + 32 * kq) * 2 : 0x40000000;
-  v4u xv[KTW][4];  // live one k-tile at a time
+  // request p of a k-tile loads rows 4p .. 4p+3, 16 lanes a row and 16 B a lane (row-contiguous); absent
+  // tokens read zeros
+  int xso[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) xv[0][q] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + q * 16, 0, 0);
+  for (int p = 0; p < 4; ++p) {
+    const int row = 4 * p + (lane >> 4);
+    xso[p] = row < M ? (row * K + 128 * kt0) * 2 + (lane & 15) * 16 : 0x40000000;
+  }
+  v4u xl[4], xv[4];
+  auto load_x = [&](int j) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) xl[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, xso[p] + 256 * j, 0, 0);
+  };
+  load_x(0);
   // scale dwords of k groups kgA .. kgA + 2 (KTW <= 8 consecutive k-tiles span at most three groups)
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(wsf + (int64_t)g0 * KG * 256), (short)0, ng * KG * 256, 0x00020000);
@@ -527,15 +542,24 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
 #pragma unroll
   for (int i = 0; i < TOT; ++i) {
     const int g = i % NG, j = i / NG, kt = kt0 + j;
-    if (g == 0 && j + 1 < KTW) {
+    if (g == 0) {
+      // x of k-tile j through the wave's LDS: written as loaded, 16-byte chunk h of row r at h ^ r (the 16
+      // rows' reads of one chunk then hit distinct banks), read back as operand pieces
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int row = 4 * p + (lane >> 4);
+        *reinterpret_cast<v4u*>(&xst[wave][row * 256 + (((lane & 15) ^ row) << 4)]) = xl[p];
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        xv[j + 1][q] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + (j + 1) * 256 + q * 16, 0, 0);
+        xv[q] = *reinterpret_cast<const v4u*>(&xst[wave][c * 256 + (((4 * kq + q) ^ c) << 4)]);
+      if (j + 1 < KTW) load_x(j + 1);
     }
     const v4u wv = buf[i % D];
     // row groups past the workgroup's share were loaded as zeros (requests keep one fixed order); their
-    // conversions and products are skipped (a uniform branch)
-    if (g < ng) {
+    // conversions and products are skipped (a uniform branch). Every share holds row group 0, and testing
+    // it at compile time keeps the compiler from sinking item 0's request into the branch behind a full wait.
+    if (g == 0 || g < ng) {
       const float s = fp4_cvt_scale((sdw[g][(kt >> 2) - kgA] >> (8 * (kt & 3))) & 0xffu);
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
@@ -546,7 +570,7 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
         v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
         v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
         acc[g][jj & 1] =
-            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, xv[j][jj]), acc[g][jj & 1], 0, 0, 0);
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, xv[jj]), acc[g][jj & 1], 0, 0, 0);
       }
     }
     if (i + D < TOT) buf[i % D] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff(i + D), 0, 2);
