@@ -493,15 +493,14 @@ extern "C" int kern_mxfp4_gemm_bf16(const void* a_, const void* sf_a, const void
   REQUIRE((int64_t)M * k < ((int64_t)1 << 32), "mxfp4_gemm_bf16: activations [M, k] must stay below 4 GiB (M=%d k=%d)",
           M, k);
   if (M == 0) return KERN_OK;
-  // M <= 32 tokens with K = 1024 * {1, 2, 4, 7, 8}: the persistent walk over the weights, about 256
+  // M <= 64 tokens with K = 1024 * {1, 2, 4, 7, 8}: the persistent walk over the weights, about 256
   // workgroups of 8 waves with hb <= 9 half groups of 8 weight rows each (the tiled grid has one workgroup
-  // per 256 weight rows, 36 at N = 9216). N = 7168, K = 8192, M = 17: 15.0 against 18.9 us; N = 9216,
-  // K = 7168, M = 32: 16.5 against 17.2. Each further 16-token group adds about 5 us to the walk, so
-  // M = 64 stays tiled (25.8 against 24.9 us).
+  // per 256 weight rows, 36 at N = 9216). Config 5 at M = 64: 17.0 against 24.9 us (N = 9216, K = 7168),
+  // 16.3 against 27.8 (N = 7168, K = 8192).
   static const char* const skinny[9] = {nullptr, "kern_mx_gemm_bf16_s1", "kern_mx_gemm_bf16_s2", nullptr,
                                         "kern_mx_gemm_bf16_s4", nullptr, nullptr, "kern_mx_gemm_bf16_s7",
                                         "kern_mx_gemm_bf16_s8"};
-  if (M <= 32 && k % 1024 == 0 && k / 1024 <= 8 && skinny[k / 1024]) {
+  if (M <= 64 && k % 1024 == 0 && k / 1024 <= 8 && skinny[k / 1024]) {
     const int32_t H = m / 8;
     const int32_t hb = std::min<int32_t>(9, (H + 255) / 256);
     Args a;

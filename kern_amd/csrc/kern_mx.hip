@@ -606,23 +606,27 @@ GEMV_PERSISTENT(7)
 GEMV_PERSISTENT(8)
 #undef GEMV_PERSISTENT
 
-// ------------------------------------- dense MXFP4 x MXFP8 -> bf16 at M <= 32 tokens: the persistent walk
-// The tiled GEMM gives a small batch one workgroup per 256 weight rows (36 at N = 9216). This kernel
-// (up to four 16-token groups; the C ABI sends it at most two) walks the weights as gemv_persistent
-// does (about 256 workgroups of 8 waves, hb <= 9 half groups each, wave w owning k-tiles
-// [w*KTW, (w+1)*KTW) of K = 1024*KTW,
-// k-tile by k-tile across the row groups, fragments six ahead) and multiplies them in their fp4 form on the
-// block-scaled MFMA against the MXFP8 activations of four 16-token groups, fetched one k-tile ahead into
-// registers: lane (c, q) of group tg holds token 16*tg + c's bytes [16q, 16q + 16) and [64 + 16q, +16) of the
-// k-tile (the 8-bit operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4) and its k block q's scale
-// byte; absent tokens read zeros. Both scale operands arrive shifted to byte 0 (OPSEL 0). The eight partial
-// sums meet in LDS one token group at a time; dbg (if not null) receives the f32 sums the bf16 values round.
+// ------------------------------------- dense MXFP4 x MXFP8 -> bf16 at M <= 64 tokens: the persistent walk
+// The tiled GEMM gives a small batch one workgroup per 256 weight rows (36 at N = 9216, which read the
+// weights at about 1.2 TB/s). This kernel walks the weights as gemv_persistent does (about 256 workgroups
+// of 8 waves, hb <= 9 half groups each, wave w owning k-tiles [w*KTW, (w+1)*KTW) of K = 1024*KTW, k-tile
+// by k-tile across the row groups, fragments four ahead) and multiplies them in their fp4 form on the
+// block-scaled MFMA against the MXFP8 activations of four 16-token groups. Lane (c, q) of group tg takes
+// token 16*tg + c's bytes [16q, 16q + 16) and [64 + 16q, +16) of the k-tile (the 8-bit operand layout of
+// V_MFMA_SCALE_F32_16X16X128_F8F6F4) and its k block q's scale byte, both through the wave's LDS: the
+// k-tile's rows are requested row-contiguous one k-tile ahead, and the scale bytes of the wave's k groups
+// once. Requested straight in operand pieces, each request gathered 16 rows (M = 64, N = 9216: 25.8
+// against 17.0 us). Both scale operands arrive shifted to byte 0 (OPSEL 0). The eight partial sums meet
+// in LDS one token group at a time; dbg (if not null) receives the f32 sums the bf16 values round.
 template <int KTW>
 KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __restrict__ wsf,
                                const uint8_t* __restrict__ xq, const uint8_t* __restrict__ xsf,
                                uint16_t* __restrict__ y, float* __restrict__ dbg, int M, int N, int K, int hb) {
-  constexpr int NG = 5, D = 6, TOT = NG * KTW, TG = 4;
+  constexpr int NG = 5, D = 4, TOT = NG * KTW, TG = 4;
+  constexpr int NS = (KTW + 6) / 4;  // k groups a wave's k-tiles touch (KTW <= 8: at most three)
   __shared__ v4f red[8][NG][64];
+  __shared__ __attribute__((aligned(16))) uint8_t xst[8][8192];      // per wave: one k-tile of 64 token rows
+  __shared__ __attribute__((aligned(16))) uint8_t sst[8][NS][1024];  // per wave: 64 rows' 16 scale bytes a k group
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KT = K >> 7, KG = K >> 9, KB = K >> 5;
   const int H = N >> 3;
@@ -632,28 +636,35 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
   const int kt0 = wave * KTW, kgA = kt0 >> 2;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, M * K, 0x00020000);
   const __amdgpu_buffer_rsrc_t xsr = __builtin_amdgcn_make_buffer_rsrc((void*)xsf, (short)0, M * KB, 0x00020000);
-  int xo[TG], so[TG];
+  // activations are requested row-contiguous: request p of a k-tile loads token rows 8p .. 8p+7, 8 lanes a
+  // 128-byte row; they pass through the wave's LDS (16-byte chunk h of row r at h ^ ((r >> 1) & 7)) and are
+  // read back as operand pieces. Scale bytes: the wave's NS k groups, one 16-byte request per row each,
+  // staged once. Absent tokens and k groups read zeros.
+  int xo[8];
 #pragma unroll
-  for (int tg = 0; tg < TG; ++tg) {
-    const int t = 16 * tg + c;
-    xo[tg] = t < M ? t * K + 128 * kt0 + 16 * q : 0x40000000;
-    so[tg] = t < M ? t * KB + 4 * kt0 : 0x40000000;
+  for (int p = 0; p < 8; ++p) {
+    const int row = 8 * p + (lane >> 3);
+    xo[p] = row < M ? row * K + 128 * kt0 + 16 * (lane & 7) : 0x40000000;
   }
-  v4u xa[KTW][TG], xb[KTW][TG];  // live one k-tile at a time
-  uint32_t xs[KTW][TG];
+  v4u xl[8];
   auto load_x = [&](int j) {
 #pragma unroll
-    for (int tg = 0; tg < TG; ++tg) {
-      xa[j][tg] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[tg] + 128 * j, 0, 0);
-      xb[j][tg] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[tg] + 128 * j + 64, 0, 0);
-      xs[j][tg] = __builtin_amdgcn_raw_buffer_load_b32(xsr, so[tg] + 4 * j, 0, 0);
-    }
+    for (int p = 0; p < 8; ++p) xl[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[p] + 128 * j, 0, 0);
   };
+  {
+    v4u sl[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+      sl[t] = __builtin_amdgcn_raw_buffer_load_b128(xsr, (lane < M && kgA + t < KG) ? lane * KB + 16 * (kgA + t)
+                                                                                      : 0x40000000, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) *reinterpret_cast<v4u*>(&sst[wave][t][lane * 16]) = sl[t];
+  }
   load_x(0);
+  v4u xa[TG], xb[TG];
   // weight-scale dwords of k groups kgA .. kgA + 2 (KTW <= 8 consecutive k-tiles span at most three groups)
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(wsf + (int64_t)g0 * KG * 256), (short)0, ng * KG * 256, 0x00020000);
-  constexpr int NS = (KTW + 6) / 4;
   uint32_t sdw[NG][NS];
 #pragma unroll
   for (int g = 0; g < NG; ++g)
@@ -680,17 +691,34 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
 #pragma unroll
   for (int i = 0; i < TOT; ++i) {
     const int g = i % NG, j = i / NG, kt = kt0 + j;
-    if (g == 0 && j + 1 < KTW) load_x(j + 1);
+    uint32_t xs[TG];
+    if (g == 0) {
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const int row = 8 * p + (lane >> 3);
+        *reinterpret_cast<v4u*>(&xst[wave][row * 128 + (((lane & 7) ^ ((row >> 1) & 7)) << 4)]) = xl[p];
+      }
+#pragma unroll
+      for (int tg = 0; tg < TG; ++tg) {
+        const int row = 16 * tg + c, sw = (row >> 1) & 7;
+        xa[tg] = *reinterpret_cast<const v4u*>(&xst[wave][row * 128 + ((q ^ sw) << 4)]);
+        xb[tg] = *reinterpret_cast<const v4u*>(&xst[wave][row * 128 + (((q + 4) ^ sw) << 4)]);
+      }
+      if (j + 1 < KTW) load_x(j + 1);
+    }
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg)
+      xs[tg] = *reinterpret_cast<const uint32_t*>(&sst[wave][(kt >> 2) - kgA][(16 * tg + c) * 16 + 4 * (kt & 3)]);
     const v4u wv = buf[i % D];
-    if (g < ng) {
+    if (g == 0 || g < ng) {
       const int sw = (int)(sdw[g][(kt >> 2) - kgA] >> (8 * (kt & 3)));
       const v8i a = {(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3], 0, 0, 0, 0};
 #pragma unroll
       for (int tg = 0; tg < TG; ++tg) {
         if (16 * tg >= M) break;  // token groups with no token (uniform)
-        const v4u lo = xa[j][tg], hi = xb[j][tg];
+        const v4u lo = xa[tg], hi = xb[tg];
         const v8i b = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        const int sx = (int)(xs[j][tg] >> (8 * q));
+        const int sx = (int)(xs[tg] >> (8 * q));
         acc[g][tg] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[g][tg], 4, 0, 0, sw, 0, sx);
       }
     }

@@ -35,14 +35,14 @@ def ops():
     return ops
 
 
-# kern_mxfp4_gemm_bf16 takes the persistent walk (kern_mx_gemm_bf16_s{k/1024}) at M <= 32 with k = 1024 *
-# {1, 2, 4, 7, 8}, else the tiled GEMM (config 5's M = 64 and 2048). The cases reach every persistent
-# instance with ragged token groups (M = 1, 17, 25, 32), half-group shares of 1, 2, 3 and 9 with a ragged
-# last workgroup (m = 4352: 544 half groups in shares of 3), and the tiled side of both bounds (M = 33;
-# k = 3072).
+# kern_mxfp4_gemm_bf16 takes the persistent walk (kern_mx_gemm_bf16_s{k/1024}) at M <= 64 with k = 1024 *
+# {1, 2, 4, 7, 8} (config 5's M = 64), else the tiled GEMM (config 5's M = 2048). The cases reach every
+# persistent instance with ragged token groups (M = 1, 17, 33, 50), half-group shares of 1, 2, 3 and 9
+# with a ragged last workgroup (m = 4352: 544 half groups in shares of 3), and the tiled side of both
+# bounds (M = 65; k = 3072).
 @pytest.mark.parametrize("M,m,k", [(64, QKV, H), (64, H, OIN), (2048, QKV, H), (2048, H, OIN),
-                                   (17, 256, 1024), (32, 4352, 2048), (25, 2304, 4096), (1, 512, 8192),
-                                   (32, 18432, 7168), (33, 2304, 4096), (24, 768, 3072)])
+                                   (17, 256, 1024), (33, 4352, 2048), (50, 2304, 4096), (1, 512, 8192),
+                                   (64, 18432, 7168), (65, 2304, 4096), (40, 768, 3072)])
 def test_gemm_bf16_config5_shapes(ops, oracle, M, m, k):
     print(f"[gemm bf16] M={M} m={m} k={k}", flush=True)
     w_raw, s_raw = _moe.gpu_raw_weights(ops, torch, 700 + m + k, 1, m, k, 119, 6)
