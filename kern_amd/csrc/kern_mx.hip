@@ -499,7 +499,8 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
   // x: lane (c, kq) holds x[c][128*kt + 32*kq .. +32] for each of its k-tiles (absent tokens: zeros)
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, 0x00020000);
   // request p of a k-tile loads rows 4p .. 4p+3, 16 lanes a row and 16 B a lane (row-contiguous); absent
-  // tokens read zeros
+  // tokens read zeros, and requests with no present token are not sent (their LDS rows keep stale bytes,
+  // which reach only the MFMA columns of absent tokens, never stored: M = 4, 13.3 -> 12.8 us)
   int xso[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
@@ -509,7 +510,8 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
   v4u xl[4], xv[4];
   auto load_x = [&](int j) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) xl[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, xso[p] + 256 * j, 0, 0);
+    for (int p = 0; p < 4; ++p)
+      if (4 * p < M) xl[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, xso[p] + 256 * j, 0, 0);
   };
   load_x(0);
   // scale dwords of k groups kgA .. kgA + 2 (KTW <= 8 consecutive k-tiles span at most three groups)
@@ -548,7 +550,7 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         const int row = 4 * p + (lane >> 4);
-        *reinterpret_cast<v4u*>(&xst[wave][row * 256 + (((lane & 15) ^ row) << 4)]) = xl[p];
+        if (4 * p < M) *reinterpret_cast<v4u*>(&xst[wave][row * 256 + (((lane & 15) ^ row) << 4)]) = xl[p];
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
