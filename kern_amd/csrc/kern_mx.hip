@@ -641,7 +641,8 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
   // activations are requested row-contiguous: request p of a k-tile loads token rows 8p .. 8p+7, 8 lanes a
   // 128-byte row; they pass through the wave's LDS (16-byte chunk h of row r at h ^ ((r >> 1) & 7)) and are
   // read back as operand pieces. Scale bytes: the wave's NS k groups, one 16-byte request per row each,
-  // staged once. Absent tokens and k groups read zeros.
+  // staged once. Absent tokens and k groups read zeros; requests with no present token are not sent (their
+  // LDS rows reach only the MFMA columns of absent tokens, never stored).
   int xo[8];
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
@@ -651,7 +652,8 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
   v4u xl[8];
   auto load_x = [&](int j) {
 #pragma unroll
-    for (int p = 0; p < 8; ++p) xl[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[p] + 128 * j, 0, 0);
+    for (int p = 0; p < 8; ++p)
+      if (8 * p < M) xl[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, xo[p] + 128 * j, 0, 0);
   };
   {
     v4u sl[NS];
@@ -698,7 +700,7 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
 #pragma unroll
       for (int p = 0; p < 8; ++p) {
         const int row = 8 * p + (lane >> 3);
-        *reinterpret_cast<v4u*>(&xst[wave][row * 128 + (((lane & 7) ^ ((row >> 1) & 7)) << 4)]) = xl[p];
+        if (8 * p < M) *reinterpret_cast<v4u*>(&xst[wave][row * 128 + (((lane & 7) ^ ((row >> 1) & 7)) << 4)]) = xl[p];
       }
 #pragma unroll
       for (int tg = 0; tg < TG; ++tg) {
