@@ -59,7 +59,8 @@ def check_fc1(torch, oracle, wp, sfp, xq, xqs, tabs, alpha, beta, m, K, c, sf_c,
     """FC1 over every live slot: gate and up accumulators within the north-star tolerance of the oracle
     (gathered activation rows, gated weight rows); SiTU-GLU on the kernel's accumulators within f32
     rounding of the formula (probe.py:46-47); e4m3 codes and ue8m0 sf_c (R128c4) bit-exact against the
-    oracle quantizer on the kernel's own SiTU values."""
+    oracle quantizer on the kernel's own SiTU values. c / sf_c are a production launch's (no debug
+    output), dbg the values of its debug twin (fc1_debug_twin)."""
     rows = c.shape[0]
     half = m // 2
     a, sa, sub, al, be = compact_experts(torch, wp, sfp, tabs, alpha, beta)
@@ -84,6 +85,23 @@ def check_fc1(torch, oracle, wp, sfp, xq, xqs, tabs, alpha, beta, m, K, c, sf_c,
     b = np.arange(kb)[None, :]
     offs = 512 * ((pv[:, None] // 128) * kb4 + b // 4) + (pv[:, None] % 32) * 16 + ((pv[:, None] % 128) // 32) * 4 + b % 4
     np.testing.assert_array_equal(to_np(sf_c)[offs], sref, err_msg=f"{what}: fc1 sf_c")
+
+
+def fc1_debug_twin(torch, launch, c, sf_c, what):
+    """FC1 as production launches it (no debug output) has written c / sf_c. Launch it again on the same
+    inputs with the debug output into fresh buffers and require its codes and scales to be bit-identical to
+    the production ones over the whole buffers: the debug stores are extra vector-memory operations, which
+    make the ring's hand-counted waits stricter, so a production wait one short would show here. Returns
+    the debug launch's [rows, 3, m/2] gate / up / SiTU values for check_fc1, which then compares the
+    production codes with the oracle."""
+    rows, half = c.shape
+    c_d, sf_d = torch.zeros_like(c), torch.zeros_like(sf_c)
+    dbg = torch.zeros((rows, 3, half), dtype=torch.float32, device=c.device)
+    launch(c_d, sf_d, dbg)
+    torch.cuda.synchronize()
+    assert torch.equal(c_d, c), f"{what}: fc1 codes with and without the debug output differ"
+    assert torch.equal(sf_d, sf_c), f"{what}: fc1 sf_c with and without the debug output differ"
+    return dbg
 
 
 def check_fc2(torch, oracle, wp, sfp, b, sfb_r128c4, tabs, m, K, c, what):

@@ -149,15 +149,19 @@ def test_moe_layer_chain(oracle, name):
     qs = torch.empty((T, H // 32), dtype=u8, device="cuda")
     c1 = torch.zeros((rows, I), dtype=u8, device="cuda")
     sf1 = torch.zeros(ops.r128c4_bytes(rows, I // 32), dtype=u8, device="cuda")
-    dbg1 = torch.zeros((rows, 3, I), dtype=torch.float32, device="cuda")
     c2 = torch.zeros((rows, H), dtype=torch.bfloat16, device="cuda")
     out = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
     ops.moe_quant(xd, q, qs, T, K=H)
     ops.moe_routing(idd, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"], tab["tp"], tab["route_map"],
                     tab["exp2perm"], tokens=T, topk=k, local_start=start, local_experts=L)
-    ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(w13, s13, q, qs, c1, sf1, tab["route_map"], to_dev(al), to_dev(be), tab["nne"],
-                                        tab["tp"], tab["cta_batch"], tab["cta_limit"], m=2 * I, k=H, ctas=ctas,
-                                        dbg=dbg1)
+    al_d, be_d = to_dev(al), to_dev(be)
+
+    def fc1(c_, sf_, dbg_):
+        ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(w13, s13, q, qs, c_, sf_, tab["route_map"], al_d, be_d, tab["nne"],
+                                            tab["tp"], tab["cta_batch"], tab["cta_limit"], m=2 * I, k=H, ctas=ctas,
+                                            dbg=dbg_)
+
+    fc1(c1, sf1, None)  # production FC1 (no debug output) feeds FC2
     ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(w2, s2, c1, sf1, c2, tab["nne"], tab["tp"], tab["cta_batch"], tab["cta_limit"],
                                       m=H, k=I, ctas=ctas)
     ops.moe_finalize(c2, tab["exp2perm"], wd, out, T, H=H, topk=k)
@@ -172,6 +176,7 @@ def test_moe_layer_chain(oracle, name):
     assert int(to_np(tab["nne"])[0]) == S
     np.testing.assert_array_equal(to_np(tab["route_map"])[: S * 128], tabs["route_map"][: S * 128])
     np.testing.assert_array_equal(to_np(tab["exp2perm"]), tabs["exp2perm"].reshape(-1))
+    dbg1 = _moe.fc1_debug_twin(torch, fc1, c1, sf1, f"layer {name}")
     _moe.check_fc1(torch, oracle, w13, s13, q, qs, tabs, al, be, 2 * I, H, c1, sf1, dbg1, f"layer {name}")
     _moe.check_fc2(torch, oracle, w2, s2, c1, sf1, tabs, H, I, c2, f"layer {name}")
     _moe.check_finalize(oracle, c2, tab["exp2perm"], wd, None, out, T, H, k, 0.0, f"layer {name}")

@@ -170,10 +170,16 @@ def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
     wp, sfp = ops.repack_weights(to_dev(w[0]), to_dev(sf[0]))
     d_scale = 1.0 / 64.0
     ds = torch.tensor([d_scale], dtype=torch.float32, device="cuda")
-    c = torch.empty((M, m), dtype=torch.uint8, device="cuda")
+    # the production launch (no debug output), then the same with the debug accumulators: the codes must be
+    # bit-identical (the debug stores make the ring's hand-counted waits stricter), and the production codes
+    # are the ones checked against the oracle below
+    c = torch.full((M, m), 0x5A, dtype=torch.uint8, device="cuda")
+    ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c, ds, M=M, m=m, k=k)
+    c_d = torch.empty((M, m), dtype=torch.uint8, device="cuda")
     dbg = torch.empty((M, m), dtype=torch.float32, device="cuda")
-    ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c, ds, M=M, m=m, k=k, dbg=dbg)
+    ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c_d, ds, M=M, m=m, k=k, dbg=dbg)
     _sync()
+    assert torch.equal(c, c_d), "e4m3 codes with and without the debug output differ"
     acc = to_np(dbg)
     qn, qsn = to_np(q), to_np(qs)
     # every row (config 3: 4096 x 2048 x 7168 takes the threaded oracle a few seconds)
@@ -365,11 +371,16 @@ def _check_fc1(ops, oracle, ids, E, m, K, local_start=0, local=None):
     half = m // 2
     c = torch.zeros((rows, half), dtype=torch.uint8, device="cuda")
     sf_c = torch.zeros(oracle.r128c4_size(rows, half // 32), dtype=torch.uint8, device="cuda")
-    dbg = torch.zeros((rows, 3, half), dtype=torch.float32, device="cuda")
-    ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(wp, sfp, q, qs, c, sf_c, dev["route_map"], to_dev(alpha), to_dev(beta),
-                                        dev["num_non_exiting"], dev["total_padded"], dev["cta_batch"],
-                                        dev["cta_limit"], m=m, k=K, ctas=ctas, dbg=dbg)
+    al_d, be_d = to_dev(alpha), to_dev(beta)
+
+    def launch(c_, sf_, dbg_):
+        ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(wp, sfp, q, qs, c_, sf_, dev["route_map"], al_d, be_d,
+                                            dev["num_non_exiting"], dev["total_padded"], dev["cta_batch"],
+                                            dev["cta_limit"], m=m, k=K, ctas=ctas, dbg=dbg_)
+
+    launch(c, sf_c, None)  # the production launch (no debug output)
     _sync()
+    dbg = _moe.fc1_debug_twin(torch, launch, c, sf_c, f"fc1 T={T} K={K}")
     print(f"[fc1] T={T} E={local} m={m} K={K}: {int(tabs['num_non_exiting'][0])} live slots", flush=True)
     _moe.check_fc1(torch, oracle, wp, sfp, q, qs, tabs, alpha, beta, m, K, c, sf_c, dbg, f"fc1 T={T} K={K}")
 
@@ -580,3 +591,113 @@ def test_mxfp8_gemm_random(ops, oracle, m, n, k):
     assert not got[:, n:].any()
     ref = oracle.mxfp8_gemm(qa, qw, ta, tw, m, n, k)
     assert_gemm_close(got[:, :n], ref, f"mxfp8 {m}x{n}x{k}")
+
+
+# --------------------------------------------------------------------------------------- high operand addresses
+
+class _HighArena:
+    """Device views whose addresses all have bit 31 of their low 32 bits set. The LDS ring's requests build a
+    wave-uniform 64-bit base in an SGPR pair from two readfirstlane halves, and a form that sign-extended the
+    low half into the high one sent an illegal address exactly when that bit was set. Views are 4 KiB
+    aligned, one after another from the first such address past the buffer's start."""
+
+    def __init__(self, nbytes):
+        self.buf = torch.empty(nbytes + (1 << 32) + 8192, dtype=torch.uint8, device="cuda")
+        base = self.buf.data_ptr()
+        lo = base & 0xFFFFFFFF
+        if lo >= (1 << 31) and lo + nbytes + 8192 <= (1 << 32):
+            start = base
+        elif lo < (1 << 31):
+            start = base - lo + (1 << 31)
+        else:
+            start = base - lo + (1 << 32) + (1 << 31)
+        self.cur, self.end = start - base, start - base + nbytes + 8192
+
+    def put(self, t):
+        n = t.numel() * t.element_size()
+        self.cur = (self.cur + 4095) & ~4095
+        assert self.cur + n <= self.end
+        v = self.buf[self.cur:self.cur + n].view(t.dtype).view(t.shape)
+        v.copy_(t)
+        a = v.data_ptr()
+        assert (a & 0xFFFFFFFF) >= (1 << 31) and ((a + max(n, 1) - 1) & 0xFFFFFFFF) >= (1 << 31), hex(a)
+        self.cur += n
+        return v
+
+
+def test_ring_operands_above_bit31(ops, oracle):
+    """The LDS-ring GEMMs with every operand and output at an address whose bit 31 is set: the config-3 mode
+    GEMM, FC1 and FC2 (slots of 20..128 rows, all on the ring) each equal the same launch on ordinary buffers
+    bit for bit; those are checked against the oracle here too (the GEMM's accumulators, FC1's codes through
+    its debug twin, FC2's rows)."""
+    from tests import _moe
+
+    arena = _HighArena(64 << 20)
+    hi = arena.put
+    # config-3 mode, dense
+    M, m, k = 300, 512, 1024
+    x = wl.activations_bf16(41, M, k, outlier_frac=0.01)
+    w, sf = wl.mxfp4_weights(42, 1, m, k, 122, 132)
+    q, qs = ops.quantize_mxfp8(to_dev(x))
+    wp, sfp = ops.repack_weights(to_dev(w[0]), to_dev(sf[0]))
+    ds = torch.tensor([1.0 / 64.0], dtype=torch.float32, device="cuda")
+    c = torch.empty((M, m), dtype=torch.uint8, device="cuda")
+    dbg = torch.empty((M, m), dtype=torch.float32, device="cuda")
+    ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c, ds, M=M, m=m, k=k, dbg=dbg)
+    c_hi = hi(torch.zeros_like(c))
+    ops.mxfp4_gemm_e4m3(hi(wp), hi(sfp), hi(q), hi(qs), c_hi, hi(ds), M=M, m=m, k=k)
+    _sync()
+    print("[bit 31] e4m3 GEMM", flush=True)
+    _, ref_acc = oracle.gemm_e4m3_pt(to_np(wp), to_np(sfp), to_np(q), to_np(qs), m, k, 1.0 / 64.0)
+    assert_gemm_close(to_np(dbg), ref_acc, "bit 31: e4m3 acc")
+    np.testing.assert_array_equal(to_np(c), oracle.e4m3_from_f32(to_np(dbg) * np.float32(1.0 / 64.0)))
+    assert torch.equal(c_hi, c), "bit 31: e4m3 GEMM output differs"
+
+    # FC1 then FC2 on its output: every slot on the ring
+    ids = _ring_row_ids()
+    E, m1, K1, m2 = 8, 2048, 1024, 512
+    T = ids.shape[0]
+    ctas, tabs, dev = _route(ops, oracle, ids, 0, E)
+    rows = ctas * 128
+    xq, xqs = ops.quantize_mxfp8(to_dev(wl.activations_bf16(43, T, K1)))
+    w1, s1 = _moe.gpu_raw_weights(ops, torch, 44, E, m1, K1, 119, 6)
+    w1p, s1p = ops.repack_weights(w1, s1, gated=True)
+    w2, s2 = _moe.gpu_raw_weights(ops, torch, 45, E, m2, m1 // 2, 118, 9)
+    w2p, s2p = ops.repack_weights(w2, s2)
+    alpha = np.full(E, 4.0, np.float32)
+    beta = np.full(E, 25.0, np.float32)
+    al, be = to_dev(alpha), to_dev(beta)
+    tab_hi = {n: hi(v) for n, v in dev.items()}
+
+    def fc1(args, c_, sf_, dbg_=None):
+        wa, sa, b, sb, rm, a_, b_, t = args
+        ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(wa, sa, b, sb, c_, sf_, rm, a_, b_, t["num_non_exiting"],
+                                            t["total_padded"], t["cta_batch"], t["cta_limit"], m=m1, k=K1, ctas=ctas,
+                                            dbg=dbg_)
+
+    lo_args = (w1p, s1p, xq, xqs, dev["route_map"], al, be, dev)
+    hi_args = (hi(w1p), hi(s1p), hi(xq), hi(xqs), tab_hi["route_map"], hi(al), hi(be), tab_hi)
+    c1 = torch.zeros((rows, m1 // 2), dtype=torch.uint8, device="cuda")
+    sf1 = torch.zeros(oracle.r128c4_size(rows, m1 // 64), dtype=torch.uint8, device="cuda")
+    fc1(lo_args, c1, sf1)
+    c1_hi, sf1_hi = hi(torch.zeros_like(c1)), hi(torch.zeros_like(sf1))
+    fc1(hi_args, c1_hi, sf1_hi)
+    _sync()
+    print("[bit 31] FC1", flush=True)
+    assert torch.equal(c1_hi, c1) and torch.equal(sf1_hi, sf1), "bit 31: FC1 output differs"
+    dbg1 = _moe.fc1_debug_twin(torch, lambda c_, s_, d_: fc1(lo_args, c_, s_, d_), c1, sf1, "bit 31 fc1")
+    _moe.check_fc1(torch, oracle, w1p, s1p, xq, xqs, tabs, alpha, beta, m1, K1, c1, sf1, dbg1, "bit 31 fc1")
+
+    def fc2(wa, sa, b, sb, c_, t):
+        ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(wa, sa, b, sb, c_, t["num_non_exiting"], t["total_padded"],
+                                          t["cta_batch"], t["cta_limit"], m=m2, k=m1 // 2, ctas=ctas,
+                                          sf_b_r128c4=True)
+
+    c2 = torch.zeros((rows, m2), dtype=torch.bfloat16, device="cuda")
+    fc2(w2p, s2p, c1, sf1, c2, dev)
+    c2_hi = hi(torch.zeros_like(c2))
+    fc2(hi(w2p), hi(s2p), c1_hi, sf1_hi, c2_hi, tab_hi)
+    _sync()
+    print("[bit 31] FC2", flush=True)
+    assert torch.equal(c2_hi.view(torch.int16), c2.view(torch.int16)), "bit 31: FC2 output differs"
+    _moe.check_fc2(torch, oracle, w2p, s2p, c1, sf1, tabs, m2, m1 // 2, c2, "bit 31 fc2")

@@ -71,10 +71,14 @@ def test_gemm_bf16_sweep(ops, oracle, i, M, m, k):
     wp, sp = ops.repack_weights(w_raw, s_raw)
     x = wl.activations_bf16(950 + i, M, k, outlier_frac=0.01)
     q, qs = ops.quantize_mxfp8(to_dev(x))
+    # the production launch (no debug output), then its debug twin: bit-identical outputs
     c = torch.empty((M, m), dtype=torch.bfloat16, device="cuda")
+    ops.mxfp4_gemm_bf16(wp[0], sp[0], q, qs, c, M=M, m=m, k=k)
+    c_d = torch.empty((M, m), dtype=torch.bfloat16, device="cuda")
     dbg = torch.empty((M, m), dtype=torch.float32, device="cuda")
-    ops.mxfp4_gemm_bf16(wp[0], sp[0], q, qs, c, M=M, m=m, k=k, dbg=dbg)
+    ops.mxfp4_gemm_bf16(wp[0], sp[0], q, qs, c_d, M=M, m=m, k=k, dbg=dbg)
     torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), c_d.view(torch.int16)), "bf16 output with and without the debug output differ"
     acc = to_np(dbg)
     np.testing.assert_array_equal(to_np(c), wl.f32_to_bf16_bits(acc))
     W = oracle.deq_fp4(to_np(w_raw[0]), to_np(s_raw[0]), m, k)
