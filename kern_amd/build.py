@@ -56,6 +56,9 @@ ENTRIES = {
                           "in buffer<f32>", "i32", "i32", "i32", "out buffer<f32>"],
     "kern_mx_gemm_bf16": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>",
                           "i32", "i32", "i32", "out buffer<f32>"],
+    **{f"kern_mx_gemm_bf16_s{ktw}": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>",
+                                     "out buffer<bf16>", "out buffer<f32>", "i32", "i32", "i32", "i32"]
+       for ktw in (1, 2, 4, 7, 8)},
     "kern_mx_routing": ["in buffer<i32>"] + ["out buffer<i32>"] * 7 + ["i32"] * 4,
     "kern_mx_quant_routing": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "in buffer<i32>"] +
                              ["out buffer<i32>"] * 7 + ["i32"] * 4,

@@ -366,7 +366,10 @@ extern "C" __global__ __launch_bounds__(256) void kern_mx_gemv_bf16_rg(
   }
 }
 
-// --------------------------------------------- decode GEMV, M <= 2, fixed K: the same, fully unrolled
+// --------------------------------------------- decode GEMV at fixed K: the same, fully unrolled
+// Taken (kern_mxfp4_gemv_bf16) for K = 512 * NKT while the x slices, 2*M*K bytes of dynamic LDS, fit in
+// 144 KiB, at M <= 3 or at any M <= 16 while N <= 8192; with the static ssc and red arrays (at most 5 KiB)
+// the workgroup stays below the 160 KiB of LDS.
 // For K = 512 * NKT with NKT in {2, 4, 8, 14, 16} each wave owns exactly NKT consecutive k-tiles (k-tile
 // ranges, not whole 512-wide groups) and its loop is unrolled, so the weight stream has no requests past
 // its end and no branches around them: every request is one the compiler's wait counts can see, and an
@@ -552,6 +555,7 @@ KERN_DEV void gemv_persistent(const uint16_t* __restrict__ x, const uint8_t* __r
         const int row = 4 * p + (lane >> 4);
         if (4 * p < M) *reinterpret_cast<v4u*>(&xst[wave][row * 256 + (((lane & 15) ^ row) << 4)]) = xl[p];
       }
+      WAVE_LDS_SYNC();
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         xv[q] = *reinterpret_cast<const v4u*>(&xst[wave][c * 256 + (((4 * kq + q) ^ c) << 4)]);
@@ -663,6 +667,7 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
                                                                                       : 0x40000000, 0, 0);
 #pragma unroll
     for (int t = 0; t < NS; ++t) *reinterpret_cast<v4u*>(&sst[wave][t][lane * 16]) = sl[t];
+    WAVE_LDS_SYNC();
   }
   load_x(0);
   v4u xa[TG], xb[TG];
@@ -702,6 +707,7 @@ KERN_DEV void gemm_skinny_bf16(const uint8_t* __restrict__ w, const uint8_t* __r
         const int row = 8 * p + (lane >> 3);
         if (8 * p < M) *reinterpret_cast<v4u*>(&xst[wave][row * 128 + (((lane & 7) ^ ((row >> 1) & 7)) << 4)]) = xl[p];
       }
+      WAVE_LDS_SYNC();
 #pragma unroll
       for (int tg = 0; tg < TG; ++tg) {
         const int row = 16 * tg + c, sw = (row >> 1) & 7;
@@ -912,6 +918,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
           *reinterpret_cast<uint2*>(stg + c * 128 + ((kw ^ (c & 7)) << 4) + 8 * ((g & 1) ^ (c >> 3))) =
               make_uint2(bf16x2_hw(v[0], v[1]), bf16x2_hw(v[2], v[3]));
         }
+        WAVE_LDS_SYNC();
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int r = 8 * h + rr;
@@ -971,6 +978,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
                 e4m3_hw2(v[0] * ds, v[1] * ds) | (e4m3_hw2(v[2] * ds, v[3] * ds) << 16);
           }
         }
+        WAVE_LDS_SYNC();
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           v4u d = *reinterpret_cast<const v4u*>(stg + j * 1024 + rr * 64 + ((k ^ ((rr >> 1) & 3)) << 4));
@@ -1072,6 +1080,7 @@ KERN_DEV void bmm_epilogue(const BmmArgs& A, const v4f (&acc)[4][4], int wt, int
       }
     }
     if (STAGED) {
+      WAVE_LDS_SYNC();
       const int rr = lane >> 1, k = lane & 1;
       const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(C + (int64_t)row0 * half), (short)0, max(valid, 0) * half, 0x00020000);

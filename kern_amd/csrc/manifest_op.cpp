@@ -532,7 +532,48 @@ struct Plan {
   uint32_t shared = 0;
   std::vector<unsigned char> args;
   std::vector<uint32_t> sizes;
+  std::vector<size_t> offs;  // each argument's offset in `args`
 };
+
+// The LDS-ring GEMM entries of kern_mx address their activations (launch argument 2) by 32-bit byte offsets
+// from the buffer's base, so the activations must stay below 4 GiB (the direct C-ABI entries refuse larger
+// ones). For each entry: the launch arguments giving the activation rows (times `rows_mul`) and the row
+// length k; FC1 gathers token rows through route_map, and no argument carries the token count.
+struct RingEntry {
+  const char* entry;
+  int nargs, rows_arg, rows_mul, k_arg;
+};
+const RingEntry kRingEntries[] = {
+    {"kern_mx_bmm_fc2", 14, 11, 128, 10},   // b [max_slots * 128, k]
+    {"kern_mx_gemm_e4m3", 10, 6, 1, 8},     // b [M, k]
+    {"kern_mx_gemm_bf16", 9, 5, 1, 7},      // b [M, k]
+    {"kern_mx_gemm_bf16_s1", 10, 6, 1, 8},  // xq [M, K]
+    {"kern_mx_gemm_bf16_s2", 10, 6, 1, 8},
+    {"kern_mx_gemm_bf16_s4", 10, 6, 1, 8},
+    {"kern_mx_gemm_bf16_s7", 10, 6, 1, 8},
+    {"kern_mx_gemm_bf16_s8", 10, 6, 1, 8},
+    {"kern_mx_bmm_fc1", 17, -1, 0, 14},     // b [tokens, k]: bound by the buffer (the program runtime checks it)
+};
+
+bool is_ring_entry(const std::string& e) {
+  for (const RingEntry& r : kRingEntries)
+    if (e == r.entry) return true;
+  return false;
+}
+
+bool check_ring_extent(const Launch& l, const Plan& pl, std::string& err) {
+  for (const RingEntry& r : kRingEntries) {
+    if (l.entry != r.entry || r.rows_arg < 0 || (int)pl.offs.size() != r.nargs) continue;
+    int32_t rows = 0, k = 0;
+    memcpy(&rows, pl.args.data() + pl.offs[r.rows_arg], 4);
+    memcpy(&k, pl.args.data() + pl.offs[r.k_arg], 4);
+    if ((int64_t)rows * r.rows_mul * k >= ((int64_t)1 << 32))
+      return err = "activations of " + std::to_string((int64_t)rows * r.rows_mul) + " rows x " + std::to_string(k) +
+                   " bytes reach 4 GiB (the ring addresses them by 32-bit offsets)",
+             false;
+  }
+  return true;
+}
 
 bool plan_launch(const kern_op_s& op, const Launch& l, const uint64_t* params, const Vars& vars, Plan& pl,
                  std::string& err) {
@@ -577,13 +618,27 @@ bool plan_launch(const kern_op_s& op, const Launch& l, const uint64_t* params, c
       return err = "arg #" + std::to_string(j) + ": " + err, false;
     }
     pl.sizes.push_back(lp.size);
+    pl.offs.push_back(n);
     n += lp.size;
   }
   pl.args.resize((pl.args.size() + 7) & ~(size_t)7, 0);
-  return true;
+  return check_ring_extent(l, pl, err);
 }
 
 }  // namespace
+
+// The param of the op (its JSON text) that a launch of an LDS-ring GEMM entry takes as its activations
+// (launch argument 2, when it forwards a param), or -1: the program runtime holds the buffer bound there
+// below 4 GiB.
+int kern_op_ring_activation_param(const char* op_json) {
+  kern_op_s op;
+  std::string err;
+  if (!op_json || !parse_op(op_json, op, err)) return -1;
+  for (const Launch& l : op.launches)
+    if (is_ring_entry(l.entry) && l.args.size() > 2 && !l.args[2].is_pack && l.args[2].src.kind == Src::Param)
+      return l.args[2].src.param;
+  return -1;
+}
 
 extern "C" int kern_op_create(const char* op_json, const char* module_name, kern_module mod, kern_op* out) {
   if (!op_json || !module_name || !mod || !out) return kern_amd_fail(KERN_ERR_API, "kern_op_create: null argument");

@@ -19,6 +19,17 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 #define KERN_DEV static __device__ __forceinline__
 
+// A wave's LDS writes made visible to its own lanes' later LDS reads of other lanes' data (a wave writes a
+// region of its own and reads it back in another lane order). LDS instructions of one wave execute in
+// order, so this costs no instruction; it states the cross-lane dependence to the compiler (a wavefront-
+// scope release/acquire pair around a wave barrier), which may otherwise treat the accesses as unordered.
+#define WAVE_LDS_SYNC()                                 \
+  do {                                                  \
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); \
+    __builtin_amdgcn_wave_barrier();                    \
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront"); \
+  } while (0)
+
 KERN_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
 // round-to-nearest-even f32 -> bf16 bits (NaN stays a quiet NaN)

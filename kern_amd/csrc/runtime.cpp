@@ -96,6 +96,7 @@ struct RtOp {
   std::string name;
   kern_op op = nullptr;
   std::vector<OpParam> params;
+  int ring_param = -1;  // the param an LDS-ring GEMM launch takes as activations (bound below 4 GiB)
 };
 
 size_t dtype_size(const std::string& d) {
@@ -125,6 +126,8 @@ bool parse_op_param(const std::string& s, OpParam& p) {
 std::mutex g_capture;  // graph capture is serialized process-wide (exec.rs:435-440)
 
 }  // namespace
+
+int kern_op_ring_activation_param(const char* op_json);  // manifest_op.cpp
 
 struct kern_runtime_s {
   int gpu = 0;
@@ -297,6 +300,7 @@ int parse_manifest(kern_runtime_s& rt, const char* text, const JVal& root, const
     const std::string op_text(text + kv.second.off, kv.second.len);
     if (int rc = host_only ? kern_op_verify(op_text.c_str()) : kern_op_create(op_text.c_str(), m0->s.c_str(), mod->second, &ro.op))
       return kern_amd_fail(rc, "op `%s`: %s", kv.first.c_str(), kern_last_error());
+    ro.ring_param = kern_op_ring_activation_param(op_text.c_str());
     rt.op_index[ro.name] = (int)rt.ops.size();
     rt.ops.push_back(std::move(ro));
   }
@@ -355,6 +359,11 @@ int parse_manifest(kern_runtime_s& rt, const char* text, const JVal& root, const
           if (ra.offset >= b.bytes)
             return manifest_fail("program `%s` call #%zu arg #%zu: offset past buffer `%s`", kv.first.c_str(), ci, ai,
                                  b.name.c_str());
+          // the LDS-ring GEMMs address their activations by 32-bit byte offsets from the bound address
+          if ((int)ai == op.ring_param && b.bytes - ra.offset >= ((uint64_t)1 << 32))
+            return manifest_fail("program `%s` call #%zu arg #%zu: `%s` binds %zu bytes of buffer `%s` as activations "
+                                 "of a ring GEMM, which must stay below 4 GiB", kv.first.c_str(), ci, ai,
+                                 prm.text.c_str(), (size_t)(b.bytes - ra.offset), b.name.c_str());
           // who may write and read what (types.rs:674-694, :150-155)
           const bool writes = prm.dir != 0;
           if (pg.derive && (b.kind == K_INPUT || b.kind == K_OUTPUT || b.kind == K_INOUT))

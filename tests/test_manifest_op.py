@@ -218,3 +218,16 @@ def test_call_errors(lib):
     with pytest.raises(ops.KernError) as e:  # grid.y beyond the launch limit
         ops.op_plan(tall, 0, [1] * 9, {"tokens": 1 << 20})
     assert e.value.code == 7 and "exceeds the launch limit" in str(e.value)
+
+
+def test_ring_activations_past_4gib_are_refused(lib):
+    """The LDS-ring GEMMs address activations by 32-bit byte offsets: a launch whose evaluated activation
+    extent (FC2: max_slots * 128 rows x k) reaches 4 GiB is refused, as the direct C-ABI entry refuses it."""
+    o = mf.moe_ops(7168, 2048, 256, 8)
+    params = [0x1000] * 9
+    ops.op_plan(o["moe_fc2"], 0, params, {"tokens": 8192})
+    # (256 + ceil(tokens * 8 / 128)) * 128 * 2048 >= 2^32 from tokens = 258048 on
+    with pytest.raises(ops.KernError) as e:
+        ops.op_plan(o["moe_fc2"], 0, params, {"tokens": 258048})
+    assert "4 GiB" in str(e.value)
+    ops.op_plan(o["moe_fc2"], 0, params, {"tokens": 258047 - 15})

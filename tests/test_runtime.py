@@ -72,3 +72,14 @@ def test_op_verify(good):
     bad = copy.deepcopy(good["ops"]["moe_fc2"])
     bad["impl"]["launches"][0]["args"] = bad["impl"]["launches"][0]["args"][:-1]
     assert ops.lib().kern_op_verify(json.dumps(bad).encode()) == 1
+
+
+def test_ring_activation_buffer_past_4gib(good):
+    """FC1 gathers token rows through route_map, so no launch argument bounds its activations: the runtime
+    refuses, at load, a buffer of 4 GiB or more bound as a ring GEMM's activations."""
+    m = copy.deepcopy(good)
+    m["buffers"]["q"].update(shape=[1 << 22, 1024])
+    code, msg = _code(m)
+    assert code == 1 and "below 4 GiB" in msg and "`q`" in msg, msg
+    m["buffers"]["q"].update(shape=[(1 << 22) - 1, 1024])
+    ops.Runtime.check(m)
