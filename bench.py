@@ -231,10 +231,44 @@ def bench_gemm(torch, ops, wl, stream, steps, warmup):
     samples = step_samples(torch, stream, step)
     flop = 2.0 * PM * PN * PK
     q_bytes = PM * PK * 2 + PM * PK + PM * PK // 32
+    clock = clock_probe(torch, ops, "kern_mx_gemm_e4m3", (PN // 256, PM // 128, 1), (512, 1, 1),
+                        (wp, sp, q, qs, c, d_scale, PM, PN, PK, None))
     return {
         "ms_per_step": ms_step, "wall_ms_per_step": wall, "flop": flop, "kernel_ms": k_avg,
-        "quant_ms": q_avg, "quant_bytes": q_bytes, "tensors": (wp, sp, q, qs), "samples": samples,
+        "quant_ms": q_avg, "quant_bytes": q_bytes, "tensors": (wp, sp, q, qs), "samples": samples, "clock": clock,
     }
+
+
+_CLOCK_MOD = []
+
+
+def clock_probe(torch, ops, entry, grid, block, args, launches=30):
+    """The shader clock a ring GEMM runs at: `entry` of the clock-probe build of kern_mx.hip (the same kernels;
+    their dbg argument carries each workgroup's s_memtime / s_memrealtime stamps at start and end, replacing
+    args[-1]), launched back to back `launches` times so that the chip is in its steady power state; the last
+    launch's stamps give each workgroup's cycles, duration and cycles / duration."""
+    import numpy as np
+
+    from kern_amd import build as kb
+
+    if not _CLOCK_MOD:
+        _CLOCK_MOD.append(ops.Module(kb.CLOCK, kb.pinned_sha256("kern_mx_clock")))
+    mod = _CLOCK_MOD[0]
+    nwg = grid[0] * (grid[1] if len(grid) > 1 else 1)
+    stamps = torch.zeros(4 * nwg, dtype=torch.int64, device="cuda")
+    for _ in range(launches):
+        mod.launch(entry, grid, block, *args[:-1], stamps)
+    torch.cuda.synchronize()
+    t = stamps.view(nwg, 4).cpu().numpy().astype(np.int64)
+    cyc, rt = t[:, 1] - t[:, 0], t[:, 3] - t[:, 2]
+    ok = rt > 0
+    ghz = cyc[ok] / rt[ok] * 0.1  # s_memrealtime ticks at 100 MHz
+    return {"kernel": entry, "workgroups": int(nwg), "shader_clock_GHz": round(float(np.median(ghz)), 3),
+            "shader_clock_GHz_min": round(float(ghz.min()), 3),
+            "workgroup_us": round(float(np.median(rt[ok])) / 100.0, 2),
+            "workgroup_cycles": int(np.median(cyc[ok])),
+            "source": "kern_amd/lib/kern_mx_clock.hsaco (kern_mx.hip built with -DKERN_CLOCK_PROBE), "
+                      f"last of {launches} back-to-back launches"}
 
 
 def bench_decode(torch, ops, wl, stream, steps, warmup, Ms):
@@ -325,6 +359,12 @@ def bench_k3(torch, ops, wl, stream, steps, warmup):
     ms2, _ = timed_loop(torch, stream, fc2, n, min(warmup, 5))
     f1 = 2.0 * R * 2 * I * H
     f2 = 2.0 * R * H * I
+    ck1 = clock_probe(torch, ops, "kern_mx_bmm_fc1", (256, 1, 1), (512, 1, 1),
+                      (w1, s1, q, qs, c1, sf1, tab["route_map"], alpha, beta, tab["nne"], tab["total_padded"],
+                       tab["cta_batch"], tab["cta_limit"], 2 * I, H, ctas, None), launches=10)
+    ck2 = clock_probe(torch, ops, "kern_mx_bmm_fc2", (256, 1, 1), (512, 1, 1),
+                      (w2, s2, c1, sf1, c2, tab["nne"], tab["total_padded"], tab["cta_batch"], tab["cta_limit"], H, I,
+                       ctas, 1, None), launches=10)
 
     def leg(ms, flop, ref_ms, kernel):
         t = flop / (ms * 1e-3) / 1e12
@@ -336,7 +376,8 @@ def bench_k3(torch, ops, wl, stream, steps, warmup):
     return {"metric": "K3 prefill 16k MoE GEMMs, one EP4 rank's share (ms per layer)",
             "config": {"T": T, "E": E, "topk": k, "local_experts": L, "local_start": start, "H": H, "I": I,
                        "local_rows": R, "cta_slots": slots, "act": "situ(alpha=4, beta=25)"},
-            "fc1": leg(ms1, f1, 0.85, "kern_mx_bmm_fc1"), "fc2": leg(ms2, f2, 0.40, "kern_mx_bmm_fc2"),
+            "fc1": dict(leg(ms1, f1, 0.85, "kern_mx_bmm_fc1"), clock=ck1),
+            "fc2": dict(leg(ms2, f2, 0.40, "kern_mx_bmm_fc2"), clock=ck2),
             "gb300_source": "docs/roadmap.md:63 (trtllm_bmm picks, tile 128)"}
 
 
@@ -770,7 +811,8 @@ def main():
                          "algorithmic_flop": g["flop"],
                          "peak_fp8_rate": PEAK_FP8_TFLOPS, "frac_fp8_rate": round(kt / PEAK_FP8_TFLOPS, 4),
                          "measured_peak": None if pk is None else pk["mfma16_fp4_fp8_TFLOPs"],
-                         "frac_measured_peak": None if pk is None else round(kt / pk["mfma16_fp4_fp8_TFLOPs"], 4)},
+                         "frac_measured_peak": None if pk is None else round(kt / pk["mfma16_fp4_fp8_TFLOPs"], 4),
+                         "clock": g["clock"]},
             "samples": g["samples"],
             "quantizer": {"kernel": "kern_mx_quant_bf16", "kernel_us": round(g["quant_ms"] * 1e3, 3),
                           "GB/s": round(g["quant_bytes"] / (g["quant_ms"] * 1e-3) / 1e9, 1),

@@ -23,6 +23,7 @@ LIBDIR = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HSACO = os.path.join(LIBDIR, "kern_mx.hsaco")
 PEAKS = os.path.join(LIBDIR, "kern_peaks.hsaco")  # roofline probes for bench.py (not on the product path)
+CLOCK = os.path.join(LIBDIR, "kern_mx_clock.hsaco")  # kern_mx.hip with its shader-clock probe (bench.py only)
 LIB = os.path.join(LIBDIR, "libkern_amd.so")
 ARCH = "gfx950"
 
@@ -120,6 +121,26 @@ def build_peaks() -> str:
     return sha
 
 
+def build_clock_probe() -> str:
+    """kern_mx.hip built with -DKERN_CLOCK_PROBE -> kern_mx_clock.hsaco, pinned in kernel_index/kern_mx_clock.toml:
+    the same kernels, with the ring GEMMs' dbg argument carrying each workgroup's shader-clock and real-time
+    stamps instead of debug values (bench.py's clock leg). Not part of the MXFP4 path."""
+    tmp = CLOCK + ".tmp"
+    flags = [f if f != "-cuid=kern_mx" else "-cuid=kern_mx_clock" for f in DEVICE_FLAGS]
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", "--no-gpu-bundle-output", *flags, "-DKERN_CLOCK_PROBE",
+          os.path.join(CSRC, "kern_mx.hip"), "-o", tmp])
+    os.replace(tmp, CLOCK)
+    with open(CLOCK, "rb") as f:
+        sha = hashlib.sha256(f.read()).hexdigest()
+    with open(os.path.join(ROOT, "kernel_index", "kern_mx_clock.toml"), "w") as f:
+        f.write("\n".join([
+            "# gfx950 shader-clock probe build of kern_amd/csrc/kern_mx.hip (-DKERN_CLOCK_PROBE) for bench.py's",
+            "# clock leg, pinned by sha256 (written by kern_amd/build.py). Not part of the MXFP4 path.",
+            "[module]", 'name = "kern_mx_clock"', 'kind = "hsaco"', f'arch = "{ARCH}"',
+            'source = "kern_amd/lib/kern_mx_clock.hsaco"', f'sha256 = "{sha}"', ""]))
+    return sha
+
+
 def pinned_sha256(name: str = "kern_mx") -> str:
     """The sha256 kernel_index/<name>.toml pins."""
     with open(os.path.join(ROOT, "kernel_index", f"{name}.toml")) as f:
@@ -183,6 +204,7 @@ def build(oracle: bool = True) -> str:
     write_index(sha)
     write_candidate(sha)
     build_peaks()
+    build_clock_probe()
     if oracle:
         build_oracle()
     return sha

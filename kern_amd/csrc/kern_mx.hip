@@ -1740,6 +1740,29 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
   }
 }
 
+// Shader-clock probe, compiled only with -DKERN_CLOCK_PROBE (kern_amd/build.py writes that build to
+// kern_amd/lib/kern_mx_clock.hsaco, a code object of its own beside the product's; bench.py loads it to read
+// the clock the ring GEMMs run at). There, the dbg argument of kern_mx_gemm_e4m3, kern_mx_bmm_fc1 and
+// kern_mx_bmm_fc2 receives no debug values but four u64 per workgroup: s_memtime (shader clock cycles) and
+// s_memrealtime (a constant 100 MHz) at the workgroup's start and end. Without the macro, nothing changes.
+#ifdef KERN_CLOCK_PROBE
+#define CLOCK_PROBE_BEGIN()                                                  \
+  const uint64_t ck_t0 = __builtin_amdgcn_s_memtime(), ck_r0 = __builtin_amdgcn_s_memrealtime()
+#define CLOCK_PROBE_END(buf)                                                                          \
+  do {                                                                                                \
+    const uint64_t ck_t1 = __builtin_amdgcn_s_memtime(), ck_r1 = __builtin_amdgcn_s_memrealtime();    \
+    if ((buf) && threadIdx.x == 0) {                                                                  \
+      uint64_t* o = reinterpret_cast<uint64_t*>(buf) + 4 * (blockIdx.x + gridDim.x * blockIdx.y);     \
+      o[0] = ck_t0, o[1] = ck_t1, o[2] = ck_r0, o[3] = ck_r1;                                         \
+    }                                                                                                 \
+  } while (0)
+#define PROBE_DBG(d) nullptr
+#else
+#define CLOCK_PROBE_BEGIN() (void)0
+#define CLOCK_PROBE_END(buf) (void)0
+#define PROBE_DBG(d) (d)
+#endif
+
 // op trtllm_bmm_bf16_mxe2m1_mxe4m3 (moe_fc2, head.json:25683; interface trtllm_bmm.py:19-27):
 // a, sf_a, b, sf_b (R128c4 when sf_b_r128c4), c bf16 [padded][m], num_non_exiting, total_padded,
 // cta_batch, cta_limit; launch adds i32 m, i32 k, i32 max_slots (the tables' capacity), i32 sf_b_r128c4,
@@ -1753,11 +1776,13 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc2(
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c;
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
-  A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = dbg;
+  A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = sf_b_r128c4; A.dbg = PROBE_DBG(dbg);
   (void)total_padded;
   // the pass's ring tiles (their expert and live rows beside them), then its small-tile quarters
   __shared__ int list[128 + 512], lexp[128], lval[128], wcnt[16];
+  CLOCK_PROBE_BEGIN();
   bmm_moe<MODE_FC2>(A, L, list, lexp, lval, wcnt);
+  CLOCK_PROBE_END(dbg);
 }
 
 // op trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (moe_fc1, head.json:25459): a, sf_a, b, sf_b (linear [T][k/32]),
@@ -1773,11 +1798,13 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.sf_c = sf_c; A.route_map = route_map;
   A.alpha = alpha; A.beta = beta;
   A.num_non_exiting = num_non_exiting; A.cta_batch = cta_batch; A.cta_limit = cta_limit;
-  A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  A.m = m; A.k = k; A.max_slots = max_slots; A.sf_b_r128c4 = 0; A.dbg = PROBE_DBG(dbg);
   (void)total_padded;
   // the pass's ring tiles (their expert and live rows beside them), then its small-tile quarters
   __shared__ int list[128 + 512], lexp[128], lval[128], wcnt[16];
+  CLOCK_PROBE_BEGIN();
   bmm_moe<MODE_FC1>(A, L, list, lexp, lval, wcnt);
+  CLOCK_PROBE_END(dbg);
 }
 
 // Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).
@@ -1790,8 +1817,10 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_e4m3(const uint8_
   BMM_LDS_DECL(L);
   BmmArgs A = {};
   A.a = a; A.sf_a = sf_a; A.b = b; A.sf_b = sf_b; A.c = c; A.d_scale = d_scale;
-  A.m = m; A.k = k; A.rows = M; A.sf_b_r128c4 = 0; A.dbg = dbg;
+  A.m = m; A.k = k; A.rows = M; A.sf_b_r128c4 = 0; A.dbg = PROBE_DBG(dbg);
+  CLOCK_PROBE_BEGIN();
   bmm_tile<MODE_PT>(A, L);
+  CLOCK_PROBE_END(dbg);
 }
 
 // Dense bf16-output mode of the FC2 family (one batch, no routing tables).
