@@ -266,6 +266,9 @@ def clock_probe(torch, ops, entry, grid, block, args, launches=30):
     return {"kernel": entry, "workgroups": int(nwg), "shader_clock_GHz": round(float(np.median(ghz)), 3),
             "shader_clock_GHz_min": round(float(ghz.min()), 3),
             "workgroup_us": round(float(np.median(rt[ok])) / 100.0, 2),
+            "workgroup_us_max": round(float(rt[ok].max()) / 100.0, 2),
+            "workgroup_us_mean": round(float(rt[ok].mean()) / 100.0, 2),
+            "span_us": round(float(t[ok, 3].max() - t[ok, 2].min()) / 100.0, 2),
             "workgroup_cycles": int(np.median(cyc[ok])),
             "source": "kern_amd/lib/kern_mx_clock.hsaco (kern_mx.hip built with -DKERN_CLOCK_PROBE), "
                       f"last of {launches} back-to-back launches"}
