@@ -369,6 +369,24 @@ def bench_k3(torch, ops, wl, stream, steps, warmup):
                       (w2, s2, c1, sf1, c2, tab["nne"], tab["total_padded"], tab["cta_batch"], tab["cta_limit"], H, I,
                        ctas, 1, None), launches=10)
 
+    # moe_routing at this size: kern_moe_routing's chunked launches (count / scan / rank over 64 workgroups),
+    # and beside it the one-workgroup kernel it takes below 16384 expanded indices, on the same tables
+    def route(i):
+        ops.moe_routing(ids, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"], tab["total_padded"],
+                        tab["route_map"], tab["exp2perm"], tokens=T, topk=k, local_start=start, local_experts=L)
+
+    from kern_amd import build as kb
+    mod = ops.Module(ops.HSACO_PATH, kb.pinned_sha256())
+    route_args = (ids, tab["counts"], tab["cta_batch"], tab["cta_limit"], tab["nne"], tab["total_padded"],
+                  tab["route_map"], tab["exp2perm"], T, k, start, L)
+    ms_r, _ = timed_loop(torch, stream, route, n, min(warmup, 5))
+    ms_r1, _ = timed_loop(torch, stream, lambda i: mod.launch("kern_mx_routing", (1, 1, 1), (1024, 1, 1),
+                                                              *route_args), n, min(warmup, 5))
+    mod.close()
+    routing = {"ms": round(ms_r, 4), "launches": "kern_mx_routing_count, _scan, _rank",
+               "one_workgroup_ms": round(ms_r1, 4), "one_workgroup_kernel": "kern_mx_routing",
+               "expanded_indices": T * k}
+
     def leg(ms, flop, ref_ms, kernel):
         t = flop / (ms * 1e-3) / 1e12
         return {"ms": round(ms, 4), "TFLOP/s": round(t, 1), "frac_fp8_rate": round(t / PEAK_FP8_TFLOPS, 4),
@@ -381,6 +399,7 @@ def bench_k3(torch, ops, wl, stream, steps, warmup):
                        "local_rows": R, "cta_slots": slots, "act": "situ(alpha=4, beta=25)"},
             "fc1": dict(leg(ms1, f1, 0.85, "kern_mx_bmm_fc1"), clock=ck1),
             "fc2": dict(leg(ms2, f2, 0.40, "kern_mx_bmm_fc2"), clock=ck2),
+            "routing": routing,
             "gb300_source": "docs/roadmap.md:63 (trtllm_bmm picks, tile 128)"}
 
 

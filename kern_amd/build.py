@@ -60,7 +60,8 @@ ENTRIES = {
     **{f"kern_mx_gemm_bf16_s{ktw}": ["in buffer<u8>", "in buffer<u8>", "in buffer<u8>", "in buffer<u8>",
                                      "out buffer<bf16>", "out buffer<f32>", "i32", "i32", "i32", "i32"]
        for ktw in (1, 2, 4, 7, 8)},
-    "kern_mx_routing": ["in buffer<i32>"] + ["out buffer<i32>"] * 7 + ["i32"] * 4,
+    **{e: ["in buffer<i32>"] + ["out buffer<i32>"] * 7 + ["i32"] * 4
+       for e in ("kern_mx_routing", "kern_mx_routing_count", "kern_mx_routing_scan", "kern_mx_routing_rank")},
     "kern_mx_quant_routing": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "in buffer<i32>"] +
                              ["out buffer<i32>"] * 7 + ["i32"] * 4,
     "kern_mx_fill_random_u8": ["out buffer<u8>", "i64", "u64", "i32", "i32"],

@@ -315,6 +315,10 @@ int launch(const char* entry, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bl
   return kern_launch(f, grid, blk, shared_bytes, stream, a.buf, (a.n + 7) & ~size_t(7));
 }
 
+// moe_routing: one workgroup below kRouteChunkedMin expanded indices, else the chunked three launches over
+// min(kRouteMaxChunks, ceil(n / kRouteChunk)) workgroups (constants shared with kern_mx.hip's routing)
+constexpr int64_t kRouteChunkedMin = 16384, kRouteChunk = 4096, kRouteMaxChunks = 64;
+
 #define REQUIRE(cond, ...) \
   do {                     \
     if (!(cond)) return fail(KERN_ERR_API, __VA_ARGS__); \
@@ -397,10 +401,18 @@ extern "C" int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_
           local_experts);
   REQUIRE(topk_idx && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm,
           "moe_routing: null buffer");
+  const int64_t n = (int64_t)tokens * topk;
+  REQUIRE(n <= INT32_MAX, "moe_routing: tokens * topk = %lld exceeds the i32 expanded indices",
+          (long long)n);
   Args a;
   a.put(topk_idx), a.put(counts), a.put(cta_batch), a.put(cta_limit), a.put(num_non_exiting), a.put(total_padded);
   a.put(route_map), a.put(exp2perm), a.put(tokens), a.put(topk), a.put(local_start), a.put(local_experts);
-  return launch("kern_mx_routing", 1, 1, 1, 1024, stream, a);
+  if (n < kRouteChunkedMin) return launch("kern_mx_routing", 1, 1, 1, 1024, stream, a);
+  // count, scan and rank over G chunks of the expanded indices (the kernels derive G from n the same way)
+  const uint32_t G = (uint32_t)std::min<int64_t>(kRouteMaxChunks, (n + kRouteChunk - 1) / kRouteChunk);
+  if (int rc = launch("kern_mx_routing_count", G, 1, 1, 1024, stream, a)) return rc;
+  if (int rc = launch("kern_mx_routing_scan", 1, 1, 1, 1024, stream, a)) return rc;
+  return launch("kern_mx_routing_rank", G, 1, 1, 1024, stream, a);
 }
 
 extern "C" int kern_moe_quant_routing(const void* x, void* q, void* sf, int32_t tokens, int32_t K,

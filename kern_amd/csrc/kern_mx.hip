@@ -2071,15 +2071,16 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8
 // ====================================================================================== routing
 // op moe_routing (head.json:25117): in i32 topk_idx[T][topk]; out counts [2E], cta_batch, cta_limit,
 // num_non_exiting[1], total_padded[1], route_map, exp2perm [T*topk]; launch adds i32 T, i32 topk,
-// i32 local_start, i32 E_local (<= 512). One workgroup of 1024 threads; rows of one expert in ascending
-// expanded index, each expert padded to 128-row CTA slots (tables as tools/kernels/abi/trtllm_bmm.py:19-27).
-// A stable counting sort with no serial step: wave w owns the w-th contiguous segment of the expanded
-// indices. (1) Each wave counts its segment per expert (LDS atomics). (2) Per expert, the counts become
-// exclusive prefixes over the waves, the slot counts an exclusive scan over the experts (wave scans), and
-// the slot tables are written. (3) Each wave walks its segment again, 64 indices at a time: the lanes
-// holding expert e OR their lane bits into a per-wave 64-bit mask, so a lane's rank among the lower lanes
-// of its expert is a popcount; the lowest such lane then advances the wave's base for e and clears the
-// mask (one wave's LDS operations execute in program order).
+// i32 local_start, i32 E_local (<= 512). Rows of one expert in ascending expanded index, each expert padded
+// to 128-row CTA slots (tables as tools/kernels/abi/trtllm_bmm.py:19-27). A stable counting sort with no
+// serial step: each wave owns a contiguous segment of the expanded indices. (1) Each wave counts its
+// segment per expert (LDS atomics). (2) Per expert, the counts become the wave's first row of the expert
+// (exclusive prefixes over the waves on top of the expert's first slot, the slot counts an exclusive scan
+// over the experts). (3) Each wave walks its segment again, 64 indices at a time: the lanes holding expert
+// e OR their lane bits into a per-wave 64-bit mask, so a lane's rank among the lower lanes of its expert is
+// a popcount; the lowest such lane then advances the wave's next row of e and clears the mask (one wave's
+// LDS operations execute in program order). kern_mx_routing does it all in one workgroup of 1024 threads;
+// kern_mx_routing_count/_scan/_rank split large batches over chunks of several workgroups.
 #define ROUTE_EMAX 512
 KERN_DEV int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -2090,13 +2091,52 @@ KERN_DEV int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// the local expert of expanded index i, or -1 when it is not local
+KERN_DEV int route_expert(const int* __restrict__ topk_idx, int i, int local_start, int E) {
+  const int e = topk_idx[i] - local_start;
+  return e >= 0 && e < E ? e : -1;
+}
+
+// phase (1) for one wave's segment [i_begin, i_end): wb[e] += the segment's indices of expert e
+KERN_DEV void route_count_wave(const int* __restrict__ topk_idx, int i_begin, int i_end, int local_start, int E,
+                               int* wb, int lane) {
+  for (int i = i_begin + lane; i < i_end; i += 64) {
+    const int e = route_expert(topk_idx, i, local_start, E);
+    if (e >= 0) atomicAdd(&wb[e], 1);
+  }
+}
+
+// phase (3) for one wave's segment: wb[e] holds the segment's first row of expert e, wm[e] is zero (and is
+// again on return)
+KERN_DEV void route_rank_wave(const int* __restrict__ topk_idx, int* __restrict__ route_map,
+                              int* __restrict__ exp2perm, int i_begin, int i_end, int topk, int local_start, int E,
+                              int* wb, unsigned long long* wm, int lane) {
+  for (int i0 = i_begin; i0 < i_end; i0 += 64) {
+    const int i = i0 + lane;
+    const int e = i < i_end ? route_expert(topk_idx, i, local_start, E) : -1;
+    if (e >= 0) atomicOr(&wm[e], 1ull << lane);
+    if (e >= 0) {
+      const unsigned long long m = wm[e];
+      const int rank = __popcll(m & ((1ull << lane) - 1ull));
+      const int p = wb[e] + rank;
+      exp2perm[i] = p;
+      route_map[p] = i / topk;
+      if (rank == 0) {  // the expert's lowest lane, after every lane of the group has read the mask
+        wb[e] += __popcll(m);
+        wm[e] = 0ull;
+      }
+    } else if (i < i_end) {
+      exp2perm[i] = -1;
+    }
+  }
+}
+
 KERN_DEV void routing_block(const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
                            int* __restrict__ cta_limit, int* __restrict__ num_non_exiting,
                            int* __restrict__ total_padded, int* __restrict__ route_map, int* __restrict__ exp2perm,
                            int T, int topk, int local_start, int E_local) {
   __shared__ int wbase[16 * ROUTE_EMAX];                 // [wave][expert]: count, then the wave's next row
   __shared__ unsigned long long wmask[16 * ROUTE_EMAX];  // [wave][expert]: lanes holding the expert
-  __shared__ int off[ROUTE_EMAX];                        // per-expert first slot
   __shared__ int wsum[16];
   __shared__ int total_slots;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -2106,16 +2146,8 @@ KERN_DEV void routing_block(const int* __restrict__ topk_idx, int* __restrict__ 
   int* wb = wbase + wave * E;
   unsigned long long* wm = wmask + wave * E;
   for (int q = lane; q < E; q += 64) wb[q] = 0, wm[q] = 0ull;
-  // the expert of expanded index i, or -1 when it is not local
-  auto expert_of = [&](int i) -> int {
-    const int e = topk_idx[i] - local_start;
-    return e >= 0 && e < E ? e : -1;
-  };
   // (1) per-wave counts (the wave's own table: the clears above came first in program order)
-  for (int i = i_begin + lane; i < i_end; i += 64) {
-    const int e = expert_of(i);
-    if (e >= 0) atomicAdd(&wb[e], 1);
-  }
+  route_count_wave(topk_idx, i_begin, i_end, local_start, E, wb, lane);
   __syncthreads();
   // (2) per expert: exclusive prefix over the waves, total count and slot count
   int cnt = 0, ns = 0;
@@ -2145,7 +2177,7 @@ KERN_DEV void routing_block(const int* __restrict__ topk_idx, int* __restrict__ 
   __syncthreads();
   if (tid < E) {
     const int o = wsum[wave] + incl - ns;
-    off[tid] = o;
+    for (int w = 0; w < 16; ++w) wbase[w * E + tid] += o * 128;  // wave w's first row of expert tid
     counts[tid] = cnt;
     counts[E + tid] = o;
     for (int s2 = 0; s2 < ns; ++s2) {
@@ -2155,26 +2187,9 @@ KERN_DEV void routing_block(const int* __restrict__ topk_idx, int* __restrict__ 
   }
   const int S = total_slots;
   for (int p = tid; p < S * 128; p += 1024) route_map[p] = -1;
-  __syncthreads();  // off[] is complete, and every padding row is written before the rows that fill it
+  __syncthreads();  // the first rows are complete, and every padding row is written before the rows that fill it
   // (3) stable ranks, 64 indices of the wave's segment at a time
-  for (int i0 = i_begin; i0 < i_end; i0 += 64) {
-    const int i = i0 + lane;
-    const int e = i < i_end ? expert_of(i) : -1;
-    if (e >= 0) atomicOr(&wm[e], 1ull << lane);
-    if (e >= 0) {
-      const unsigned long long m = wm[e];
-      const int rank = __popcll(m & ((1ull << lane) - 1ull));
-      const int p = off[e] * 128 + wb[e] + rank;
-      exp2perm[i] = p;
-      route_map[p] = i / topk;
-      if (rank == 0) {  // the expert's lowest lane, after every lane of the group has read the mask
-        wb[e] += __popcll(m);
-        wm[e] = 0ull;
-      }
-    } else if (i < i_end) {
-      exp2perm[i] = -1;
-    }
-  }
+  route_rank_wave(topk_idx, route_map, exp2perm, i_begin, i_end, topk, local_start, E, wb, wm, lane);
 }
 
 extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing(
@@ -2200,6 +2215,150 @@ extern "C" __global__ __launch_bounds__(1024) void kern_mx_quant_routing(
     return;
   }
   quant_bf16_lane(x, q, sf, T, K, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
+}
+
+// moe_routing for large batches in three launches, with kern_mx_routing's tables bit for bit. The n = T*topk
+// expanded indices split into G = min(64, ceil(n / 4096)) chunks of CH = floor(n / G) rounded down to 64
+// indices, the last chunk taking the rest; for n >= 4096 every chunk holds at least 1984 > E indices.
+// (count) workgroup g counts its chunk per expert and parks the counts in exp2perm[g*CH + e], the first E
+// entries of its own chunk. (scan) one workgroup turns the G x E counts into the slot tables and, per
+// chunk and expert, the chunk's first row of the expert, written back in the same places; it also writes
+// the padding rows of route_map. (rank) workgroup g reads its chunk's E first rows, then ranks the chunk
+// as kern_mx_routing's block ranks its segments (16 waves) and overwrites the parked entries with the
+// chunk's own exp2perm. No chunk reads another chunk's exp2perm range, so the rank workgroups do not race.
+// All three take kern_mx_routing's arguments; grid [G] for count and rank, [1] for scan, block 1024.
+// The host takes this path for n >= 4096 only.
+#define ROUTE_CHUNK 4096
+#define ROUTE_GMAX 64
+KERN_DEV int route_chunks(int n) { return min(ROUTE_GMAX, max(1, (n + ROUTE_CHUNK - 1) / ROUTE_CHUNK)); }
+KERN_DEV int route_chunk_len(int n, int G) { return (n / G) & ~63; }
+
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing_count(
+    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
+    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+  __shared__ int h[ROUTE_EMAX];
+  const int tid = threadIdx.x, n = T * topk, E = E_local, G = route_chunks(n), g = blockIdx.x;
+  if (g >= G) return;
+  const int CH = route_chunk_len(n, G), b = g * CH, end = g == G - 1 ? n : b + CH;
+  if (tid < E) h[tid] = 0;
+  __syncthreads();
+  for (int i = b + tid; i < end; i += 1024) {
+    const int e = route_expert(topk_idx, i, local_start, E);
+    if (e >= 0) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  if (tid < E && b + tid < end) exp2perm[b + tid] = h[tid];
+}
+
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing_scan(
+    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
+    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+  __shared__ int h[ROUTE_GMAX * ROUTE_EMAX];  // [chunk][expert]: count, then the chunk's first row (128 KiB)
+  __shared__ int off[ROUTE_EMAX], cnt_e[ROUTE_EMAX];
+  __shared__ int wsum[16];
+  __shared__ int total_slots;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = T * topk, E = E_local, G = route_chunks(n), CH = route_chunk_len(n, G);
+  for (int q = tid; q < G * E; q += 1024) {
+    const int g = q / E, i = g * CH + (q - g * E);
+    h[q] = i < n ? exp2perm[i] : 0;
+  }
+  __syncthreads();
+  // per expert: exclusive prefix over the chunks (eight loads before their stores), total and slot count
+  int cnt = 0, ns = 0;
+  if (tid < E) {
+    for (int g0 = 0; g0 < G; g0 += 8) {
+      int c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = g0 + j < G ? h[(g0 + j) * E + tid] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (g0 + j < G) h[(g0 + j) * E + tid] = cnt;
+        cnt += c[j];
+      }
+    }
+    ns = (cnt + 127) >> 7;
+  }
+  // exclusive scan of the slot counts over the experts (E <= 512: waves 0..7)
+  const int incl = wave_incl_scan(ns, lane);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  if (tid == 0) {
+    int s = 0;
+    for (int w = 0; w < 16; ++w) {
+      const int v = wsum[w];
+      wsum[w] = s;
+      s += v;
+    }
+    total_slots = s;
+    num_non_exiting[0] = s;
+    total_padded[0] = s * 128;
+  }
+  __syncthreads();
+  if (tid < E) {
+    const int o = wsum[wave] + incl - ns;
+    off[tid] = o;
+    cnt_e[tid] = cnt;
+    counts[tid] = cnt;
+    counts[E + tid] = o;
+  }
+  __syncthreads();
+  const int S = total_slots;
+  // slot tables, a thread per slot: the slot's expert is the last with off[e] <= s (an expert without
+  // slots shares its off with the next one, and the last expert's off + slots is S > s)
+  for (int s = tid; s < S; s += 1024) {
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= s) lo = mid;
+      else hi = mid - 1;
+    }
+    cta_batch[s] = lo;
+    cta_limit[s] = min((s + 1) * 128, off[lo] * 128 + cnt_e[lo]);
+  }
+  // padding rows, a wave per expert: rows past the count in the expert's last slot
+  for (int e = wave; e < E; e += 16) {
+    const int p0 = off[e] * 128 + cnt_e[e], p1 = (off[e] + ((cnt_e[e] + 127) >> 7)) * 128;
+    for (int p = p0 + lane; p < p1; p += 64) route_map[p] = -1;
+  }
+  // per chunk and expert: the first row, parked where the count was
+  for (int q = tid; q < G * E; q += 1024) {
+    const int g = q / E, e = q - g * E, i = g * CH + e;
+    if (i < n) exp2perm[i] = off[e] * 128 + h[q];
+  }
+}
+
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_routing_rank(
+    const int* __restrict__ topk_idx, int* __restrict__ counts, int* __restrict__ cta_batch,
+    int* __restrict__ cta_limit, int* __restrict__ num_non_exiting, int* __restrict__ total_padded,
+    int* __restrict__ route_map, int* __restrict__ exp2perm, int T, int topk, int local_start, int E_local) {
+  __shared__ int wbase[16 * ROUTE_EMAX];                 // [wave][expert]: count, then the wave's next row
+  __shared__ unsigned long long wmask[16 * ROUTE_EMAX];  // [wave][expert]: lanes holding the expert
+  __shared__ int first[ROUTE_EMAX];                      // the chunk's first row of each expert
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = T * topk, E = E_local, G = route_chunks(n), g = blockIdx.x;
+  if (g >= G) return;
+  const int CH = route_chunk_len(n, G), b = g * CH, end = g == G - 1 ? n : b + CH;
+  if (tid < E) first[tid] = b + tid < end ? exp2perm[b + tid] : 0;
+  const int seg = (end - b + 16 * 64 - 1) / (16 * 64) * 64;  // indices per wave, a multiple of 64
+  const int i_begin = b + wave * seg, i_end = min(end, i_begin + seg);
+  int* wb = wbase + wave * E;
+  unsigned long long* wm = wmask + wave * E;
+  for (int q = lane; q < E; q += 64) wb[q] = 0, wm[q] = 0ull;
+  route_count_wave(topk_idx, i_begin, i_end, local_start, E, wb, lane);
+  __syncthreads();  // every parked first row is read before any exp2perm store of the chunk; counts complete
+  if (tid < E) {
+    int r = first[tid];
+    for (int w = 0; w < 16; ++w) {
+      const int c = wbase[w * E + tid];
+      wbase[w * E + tid] = r;
+      r += c;
+    }
+  }
+  __syncthreads();
+  route_rank_wave(topk_idx, route_map, exp2perm, i_begin, i_end, topk, local_start, E, wb, wm, lane);
 }
 
 

@@ -72,21 +72,33 @@ def k3_moe_sf_shuffle(E: int, max_bytes: int) -> dict:
     }
 
 
+# moe_routing's chunked launches (kern_mx_routing_count/_scan/_rank) from this many expanded indices, over
+# min(ROUTE_MAX_CHUNKS, ceil(tokens*topk / ROUTE_CHUNK)) workgroups; the C ABI's kern_moe_routing switches at
+# the same point
+ROUTE_CHUNKED_MIN, ROUTE_CHUNK, ROUTE_MAX_CHUNKS = 16384, 4096, 64
+
+
 def moe_routing(topk: int, local_start: int, local_experts: int) -> dict:
     """moe_routing(in i32 topk_idx, out i32 counts, cta_batch, cta_limit, num_non_exiting, total_padded,
-    route_map, exp2perm); launch adds the token count (var `tokens`), top-k and the local expert range."""
+    route_map, exp2perm); launch adds the token count (var `tokens`), top-k and the local expert range.
+    One workgroup below ROUTE_CHUNKED_MIN expanded indices, else count -> scan -> rank over chunks (the same
+    tables bit for bit); `when` on `tokens` picks the launches."""
     bufs = ["in buffer<i32>"] + ["out buffer<i32>"] * 7
+    first = _ceil(ROUTE_CHUNKED_MIN, topk)  # the least token count with tokens*topk >= ROUTE_CHUNKED_MIN
+    args = [{"param": i} for i in range(8)] + [{"pack": {"size": 4, "fields": [{"at": 0, "var": "tokens"}]}},
+                                               {"i32": topk}, {"i32": local_start}, {"i32": local_experts}]
+    chunks = {"clamp": [{"ceil_div": [{"mul": ["tokens", topk]}, ROUTE_CHUNK]}, 0, ROUTE_MAX_CHUNKS]}
+
+    def launch(entry, grid, when):
+        return {"module": MODULE, "entry": entry, "params": bufs + ["bytes<4>", "i32", "i32", "i32"],
+                "block": [1024, 1, 1], "grid": [grid, 1, 1], "when": {"var": "tokens", **when}, "args": args}
+
     return {
         "params": bufs,
-        "impl": {"launches": [{
-            "module": MODULE, "entry": "kern_mx_routing",
-            "params": bufs + ["bytes<4>", "i32", "i32", "i32"],
-            "block": [1024, 1, 1],
-            "grid": [1, 1, 1],
-            "args": [{"param": i} for i in range(8)]
-            + [{"pack": {"size": 4, "fields": [{"at": 0, "var": "tokens"}]}},
-               {"i32": topk}, {"i32": local_start}, {"i32": local_experts}],
-        }]},
+        "impl": {"launches": [launch("kern_mx_routing", 1, {"max": first - 1}),
+                              launch("kern_mx_routing_count", chunks, {"min": first}),
+                              launch("kern_mx_routing_scan", 1, {"min": first}),
+                              launch("kern_mx_routing_rank", chunks, {"min": first})]},
     }
 
 

@@ -191,15 +191,23 @@ def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
 
 # --------------------------------------------------------------------------------------- routing
 
-# uniform ids; every token on the same k experts (slots of 128 rows, several per expert); the 512-expert
-# maximum; a segment per wave of several 64-index rounds (T*k = 65536); decode sizes: 64 indices (one wave's
-# round), with non-local experts, with every token on the same experts, and 65 (a second round)
+# One workgroup (T*k < 16384): uniform ids; every token on the same k experts (slots of 128 rows, several per
+# expert); the 512-expert maximum; a segment per wave of several 64-index rounds (T*k = 12288, and 16376, one
+# round below the chunked launches); decode sizes: 64 indices (one wave's round), with non-local experts,
+# with every token on the same experts, and 65 (a second round). Chunked (count / scan / rank): 16384
+# indices (4 chunks), a ragged last chunk with 512 experts (16392 = 4 x 3264 + 3336), a K3 rank (16384
+# tokens x 16 over 224 experts, 56 local: 64 chunks), 64 chunks of 8192 indices, every token on the same
+# experts, non-local experts, a single local expert.
 @pytest.mark.parametrize("T,E,k,start,local,skew", [(512, 256, 8, 0, 256, 0), (37, 16, 4, 4, 8, 0),
                                                     (1, 8, 2, 0, 8, 0), (300, 224, 16, 56, 56, 0),
                                                     (2048, 64, 6, 0, 64, 0), (1000, 64, 4, 0, 64, 1),
-                                                    (100, 512, 8, 0, 512, 0), (8192, 256, 8, 0, 256, 0),
+                                                    (100, 512, 8, 0, 512, 0), (2047, 256, 8, 0, 256, 0),
                                                     (8, 256, 8, 0, 256, 0), (4, 224, 16, 56, 56, 0),
-                                                    (8, 64, 8, 0, 64, 1), (13, 16, 5, 2, 8, 0)])
+                                                    (8, 64, 8, 0, 64, 1), (13, 16, 5, 2, 8, 0),
+                                                    (2048, 256, 8, 0, 256, 0), (2049, 512, 8, 0, 512, 0),
+                                                    (16384, 224, 16, 56, 56, 0), (65536, 256, 8, 0, 256, 0),
+                                                    (4096, 64, 4, 0, 64, 1), (3000, 256, 8, 128, 64, 0),
+                                                    (4096, 8, 4, 3, 1, 0)])
 def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
     ids = wl.topk_ids(T * 31 + E, T, E, k)
     if skew:

@@ -78,7 +78,7 @@ def test_k3_grids_match_reference():
     assert o["moe_finalize_rms"]["impl"]["launches"][0]["grid"] == g["moe_finalize_rms"]["grid"]
 
 
-@pytest.mark.parametrize("T", [1, 37, 512, 8192])
+@pytest.mark.parametrize("T", [1, 37, 512, 1023, 1024, 8192])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_plan_grids_and_kernargs(lib, shape, T):
     H, I, E, k = shape["H"], shape["I"], shape["E"], shape["k"]
@@ -90,9 +90,16 @@ def test_plan_grids_and_kernargs(lib, shape, T):
     assert p["grid"] == (-(-T * H // 8 // 512), 1, 1) and p["block"] == (256, 1, 1)
     assert p["args"] == pack([("Q", 0x1000), ("Q", 0x2000), ("Q", 0x3000), ("i", T), ("i", H)])
 
-    p = ops.op_plan(o["moe_routing"], 0, bufs(8), v)
-    assert p["grid"] == (1, 1, 1) and p["block"] == (1024, 1, 1)
-    assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(8)] + [("i", T), ("i", k), ("i", 0), ("i", E)])
+    # one workgroup below 16384 expanded indices, else count / scan / rank over min(64, ceil(T*k / 4096))
+    chunked = T * k >= 16384
+    G = min(64, -(-T * k // 4096))
+    for j, grid in enumerate([1, G, 1, G]):
+        p = ops.op_plan(o["moe_routing"], j, bufs(8), v)
+        assert p["skip"] == ((j > 0) != chunked), (j, T * k)
+        if not p["skip"]:
+            assert p["grid"] == (grid, 1, 1) and p["block"] == (1024, 1, 1)
+            assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(8)] +
+                                     [("i", T), ("i", k), ("i", 0), ("i", E)])
 
     p = ops.op_plan(o["moe_fc1"], 0, bufs(13), v)
     assert p["grid"] == (256, 1, 1) and p["block"] == (512, 1, 1)
