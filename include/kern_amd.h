@@ -150,6 +150,35 @@ int kern_op_plan(const char* op_json, int launch_index, const uint64_t* params, 
 int kern_candidate_splice(const char* manifest_json, const char* candidate_json, char* out, size_t cap,
                           size_t* out_len);
 
+/* Building candidates (candidate.rs:83-113, :231-300). Each writes a Candidate {modules, ops} (JSON,
+ * NUL-terminated; modules and ops in name order) to out[cap] and its length to *out_len; out NULL queries the
+ * length. Misfits are KERN_ERR_MANIFEST with every reason listed ("candidate does not fit: ...").
+ * kern_candidate_of (Candidate::of, :84-87): the manifest's own implementation of the n_ops ops named, with
+ * the modules they launch; an op the manifest lacks is left out.
+ * kern_candidate_only (Candidate::only, :89-97): the same cut of a candidate.
+ * kern_candidate_join (Candidate::join, :99-113): n candidates as one; an op two of them implement is refused
+ * ("op `X` is implemented twice"), and a module name two of them give to other bytes stays with the first and
+ * is renamed <name>@<sha256[0:8]> in the others.
+ * kern_candidate_tile (tile, :231-300): one implementation of `op` from n pieces, piece i running
+ * pieces[i].candidate_json's implementation while `var` is in [min, max] (an end whose has_ flag is 0 is
+ * open): each launch is narrowed to the piece's range (its own `when` on `var` intersected with it; dropped
+ * when the two miss; refused when conditioned on another var; a lower end of 1 is no bound), modules are
+ * adopted as by join, and a scratch name an earlier piece gives another dtype or shape becomes <name>@<i>,
+ * in the piece's launch args too. Ranges are the caller's: overlapping pieces both run there, and a value no
+ * piece covers runs nothing. Refused when no launch of any piece runs in its range. */
+typedef struct kern_candidate_piece {
+  const char* candidate_json;
+  int32_t has_min, has_max;
+  uint64_t min, max;
+} kern_candidate_piece;
+int kern_candidate_of(const char* manifest_json, const char* const* ops, int n_ops, char* out, size_t cap,
+                      size_t* out_len);
+int kern_candidate_only(const char* candidate_json, const char* const* ops, int n_ops, char* out, size_t cap,
+                        size_t* out_len);
+int kern_candidate_join(const char* const* candidates, int n, char* out, size_t cap, size_t* out_len);
+int kern_candidate_tile(const char* op, const char* var, const kern_candidate_piece* pieces, int n, char* out,
+                        size_t cap, size_t* out_len);
+
 /* ------------------------------------------------------------------------------------------------
  * Program runtime (kern_amd/csrc/runtime.cpp): a kern manifest's buffers, modules, ops and programs,
  * run by program name with var values, as crates/kern-runtime's Runtime (src/lib.rs:137-236) runs them.

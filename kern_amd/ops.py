@@ -104,6 +104,10 @@ _SIGS = {
     "kern_rt_time_range": [P, ctypes.c_char_p, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, P],
     "kern_rt_synchronize": [P],
     "kern_candidate_splice": [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_size_t, P],
+    "kern_candidate_of": [ctypes.c_char_p, P, ctypes.c_int, P, ctypes.c_size_t, P],
+    "kern_candidate_only": [ctypes.c_char_p, P, ctypes.c_int, P, ctypes.c_size_t, P],
+    "kern_candidate_join": [P, ctypes.c_int, P, ctypes.c_size_t, P],
+    "kern_candidate_tile": [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_int, P, ctypes.c_size_t, P],
     "kern_rt_buffer": [P, ctypes.c_char_p, P, P],
 }
 
@@ -608,6 +612,61 @@ def splice(manifest: dict | str, candidate: dict | str) -> dict:
     buf = ctypes.create_string_buffer(n.value + 1)
     check(lib().kern_candidate_splice(mt.encode(), ct.encode(), buf, n.value + 1, ctypes.byref(n)))
     return json.loads(buf.value.decode())
+
+
+def _json_text(x) -> str:
+    return x if isinstance(x, str) else json.dumps(x)
+
+
+def _strings(xs) -> tuple:
+    """A C array of NUL-terminated strings (and the encoded bytes it points into, to keep alive)."""
+    enc = [x.encode() for x in xs]
+    return (ctypes.c_char_p * max(1, len(enc)))(*enc), enc
+
+
+def _candidate_call(fn, *args) -> dict:
+    # size query, then the text
+    n = ctypes.c_size_t()
+    check(fn(*args, None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    check(fn(*args, buf, n.value + 1, ctypes.byref(n)))
+    return json.loads(buf.value.decode())
+
+
+def candidate_of(manifest: dict | str, ops: list) -> dict:
+    """Candidate::of (crates/kern-manifest/src/candidate.rs:84-87) through kern_candidate_of: the manifest's
+    own implementation of `ops`, with the modules they launch; an op the manifest lacks is left out."""
+    arr, keep = _strings(ops)
+    return _candidate_call(lib().kern_candidate_of, _json_text(manifest).encode(), ctypes.cast(arr, P), len(ops))
+
+
+def candidate_only(candidate: dict | str, ops: list) -> dict:
+    """Candidate::only (candidate.rs:89-97) through kern_candidate_only: the candidate cut down to `ops`."""
+    arr, keep = _strings(ops)
+    return _candidate_call(lib().kern_candidate_only, _json_text(candidate).encode(), ctypes.cast(arr, P), len(ops))
+
+
+def candidate_join(candidates: list) -> dict:
+    """Candidate::join (candidate.rs:99-113) through kern_candidate_join: the candidates as one;
+    KernError(KERN_ERR_MANIFEST) when two implement the same op."""
+    arr, keep = _strings([_json_text(c) for c in candidates])
+    return _candidate_call(lib().kern_candidate_join, ctypes.cast(arr, P), len(candidates))
+
+
+class _Piece(ctypes.Structure):
+    _fields_ = [("candidate_json", ctypes.c_char_p), ("has_min", ctypes.c_int32), ("has_max", ctypes.c_int32),
+                ("min", ctypes.c_uint64), ("max", ctypes.c_uint64)]
+
+
+def candidate_tile(op: str, var: str, pieces: list) -> dict:
+    """candidate::tile (candidate.rs:231-300) through kern_candidate_tile: one implementation of `op` from
+    pieces (candidate, min, max), each running its candidate's implementation while `var` is in [min, max]
+    (None = open end)."""
+    texts = [_json_text(c).encode() for c, _, _ in pieces]
+    arr = (_Piece * max(1, len(pieces)))()
+    for i, ((_, lo, hi), t) in enumerate(zip(pieces, texts)):
+        arr[i] = _Piece(t, lo is not None, hi is not None, lo or 0, hi or 0)
+    return _candidate_call(lib().kern_candidate_tile, op.encode(), var.encode(), ctypes.cast(arr, P), len(pieces))
 
 
 class Module:
