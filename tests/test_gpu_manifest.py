@@ -92,6 +92,32 @@ def test_moe_layer_through_manifest_ops(ops):
                            b[name].view(torch.uint8) if b[name].dtype == torch.bfloat16 else b[name]), name
 
 
+# moe_routing through its manifest op on both sides of the switch to the chunked launches (`when` on tokens):
+# 16376 expanded ids (one workgroup), 16384 (count / scan / rank over 4 chunks) and a K3 rank's 262144 (64
+# chunks, non-local experts); every table bit for bit against the oracle
+@pytest.mark.parametrize("T,E,k,start,local", [(2047, 256, 8, 0, 256), (2048, 256, 8, 0, 256),
+                                               (16384, 224, 16, 56, 56)])
+def test_routing_op_on_both_paths(ops, T, E, k, start, local):
+    from oracle import mxoracle as oracle
+    print(f"[manifest] moe_routing T={T} E={E} k={k} local {start}+{local}", flush=True)
+    op = ops.ManifestOp(mf.moe_routing(k, start, local))
+    ids = wl.topk_ids(T * 3 + E, T, E, k)
+    ctas = ops.ctas_bound(T, k, local)
+    ref = oracle.routing(ids, start, local, ctas_cap=ctas)
+    tabs = [torch.full((n,), -7, dtype=torch.int32, device="cuda")
+            for n in (2 * local, ctas, ctas, 1, 1, ctas * 128, T * k)]
+    op(_dev(ids), *tabs, vars={"tokens": T})
+    torch.cuda.synchronize()
+    counts, cb, cl, nne, tp, rmap, e2p = (t.cpu().numpy() for t in tabs)
+    S = int(ref["num_non_exiting"][0])
+    assert (int(nne[0]), int(tp[0])) == (S, S * 128)
+    np.testing.assert_array_equal(counts, ref["counts"])
+    np.testing.assert_array_equal(cb[:S], ref["cta_batch"][:S])
+    np.testing.assert_array_equal(cl[:S], ref["cta_limit"][:S])
+    np.testing.assert_array_equal(rmap[:S * 128], ref["route_map"][:S * 128])
+    np.testing.assert_array_equal(e2p, ref["exp2perm"].reshape(-1))
+
+
 def test_create_checks_against_code_object(ops):
     o = mf.moe_fc2(1024, 512, 8, 2)
     with pytest.raises(ops.KernError) as e:  # the manifest names another module

@@ -232,11 +232,12 @@ def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
 
 
 # moe_quant + moe_routing in one call: decode sizes and config 4 in one launch; a K3 rank's local experts
-# (ids outside the range); T*K past one launch's quantizer workgroups, which takes the two launches
+# (ids outside the range); T*K past one launch's quantizer workgroups, which takes the two launches, with
+# one-workgroup routing (T = 600) and with the chunked routing (T = 2048, 16384 expanded ids)
 @pytest.mark.parametrize("T,E,k,start,local,K", [(1, 256, 8, 0, 256, 7168), (4, 256, 8, 0, 256, 7168),
                                                  (64, 256, 8, 0, 256, 7168), (512, 256, 8, 0, 256, 7168),
                                                  (300, 224, 16, 56, 56, 3584), (600, 256, 8, 0, 256, 7168),
-                                                 (3, 8, 2, 0, 8, 96)])
+                                                 (2048, 256, 8, 0, 256, 7168), (3, 8, 2, 0, 8, 96)])
 def test_quant_routing_fused(ops, oracle, T, E, k, start, local, K):
     x = wl.activations_bf16(11 + T, T, K, outlier_frac=0.01)
     x[:min(T, 8)] = _special_rows(K)[:min(T, 8)]
