@@ -401,9 +401,10 @@ extern "C" int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_
           local_experts);
   REQUIRE(topk_idx && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm,
           "moe_routing: null buffer");
+  // expanded ids and padded rows (at most tokens * topk + 128 * local_experts) are i32 in the tables
   const int64_t n = (int64_t)tokens * topk;
-  REQUIRE(n <= INT32_MAX, "moe_routing: tokens * topk = %lld exceeds the i32 expanded indices",
-          (long long)n);
+  REQUIRE(n + 128LL * local_experts <= INT32_MAX,
+          "moe_routing: tokens * topk = %lld leaves the padded rows past the i32 tables", (long long)n);
   Args a;
   a.put(topk_idx), a.put(counts), a.put(cta_batch), a.put(cta_limit), a.put(num_non_exiting), a.put(total_padded);
   a.put(route_map), a.put(exp2perm), a.put(tokens), a.put(topk), a.put(local_start), a.put(local_experts);

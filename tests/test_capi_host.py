@@ -102,7 +102,8 @@ _NZ = ctypes.c_void_p(16)  # a non-null address that no call here dereferences (
     (lambda L: L.kern_mxfp4_gemm_e4m3(*([None] * 6), 16, 256, 500, None, None), "k % 512"),
     (lambda L: L.kern_mxfp4_gemm_bf16(*([None] * 5), -1, 256, 512, None, None), "m % 256"),
     (lambda L: L.kern_moe_routing(*([None] * 8), 4, 2, 0, 513, None), "local_experts <= 512"),
-    (lambda L: L.kern_moe_routing(*([_NZ] * 8), 1 << 28, 16, 0, 8, None), "exceeds the i32 expanded indices"),
+    (lambda L: L.kern_moe_routing(*([_NZ] * 8), 1 << 28, 16, 0, 8, None), "past the i32 tables"),
+    (lambda L: L.kern_moe_routing(*([_NZ] * 8), (2**31 - 1 - 128 * 512) // 8 + 1, 8, 0, 512, None), "past the i32 tables"),
     (lambda L: L.kern_fill_random_u8(None, 16, 1, 0, 0, None), "span"),
     # the LDS ring addresses activations by 32-bit offsets from the buffer's base: past 4 GiB is refused
     (lambda L: L.kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(*([_NZ] * 9), 256, 8192, 4200, 1, None, None), "below 4 GiB"),
