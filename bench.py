@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--decode-m 1 4 16] [--stack-m 1 64 2048]
                     [--only gemm|decode|moe|stack|mxfp8|k3|peaks|copy]
 
-Headline (BASELINE.json metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
+Headline (metric "MXFP4 GEMM TFLOP/s (% MFMA peak) M=4096; decode GB/s (% HBM peak) M=1"):
 
 * step = one pass of config 3 over resident inputs: bf16 activations [4096, 7168] (N(0,1), 1% outliers x20)
   quantised on the GPU to MXFP8 (op moe_quant), then the MXFP4 x MXFP8 GEMM against repacked weights
@@ -63,7 +63,7 @@ PEAK_MXFP4_TFLOPS = 10100.0  # MI355X dense MXFP4/MXFP6 MFMA, published
 PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, published (fp8-operand scaled MFMA rate)
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
 
-# config 3 (prefill GEMM) and config 2 (decode GEMV) shapes, BASELINE.json configs[2] / configs[1]
+# config 3 (prefill GEMM) and config 2 (decode GEMV) shapes
 PM, PN, PK = 4096, 2048, 7168
 DN, DK = 18432, 7168
 
@@ -72,10 +72,10 @@ def gemv_kernel(M):
     """The kernel kern_mxfp4_gemv_bf16 launches for config 2 (K = 7168) at M tokens."""
     return "kern_mx_gemv_bf16_r14" if M <= 3 else "kern_mx_gemv_bf16_p7"
 
-# config 4 (MoE grouped), BASELINE.json configs[3]
+# config 4 (MoE grouped)
 MT, ME, MTOP, MH, MI = 512, 256, 8, 7168, 2048
 K3_T = 16384  # K3 prefill tokens of the reference's published FC1 / FC2 timings
-# config 5 (layer stack), BASELINE.json configs[4]
+# config 5 (layer stack)
 S_LAYERS, S_QKV, S_OIN, S_MS = 4, 9216, 8192, (1, 64, 2048)
 MALL_BYTES = 256 << 20
 CPU_SHARE = 16  # host cores a one-GPU job may use on these boxes (worker pools are sized to it)

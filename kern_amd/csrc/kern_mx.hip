@@ -141,7 +141,7 @@ typedef __attribute__((address_space(1))) void glob_void_t;
 #define WAIT_LGKMCNT0 __builtin_amdgcn_s_waitcnt(0xC07F)
 
 // ====================================================================================== decode GEMV
-// op mxfp4_gemv_bf16 (new; the W4A16 decode of BASELINE configs 1-2): in bf16 x[M][K], in u8 w (repacked,
+// op mxfp4_gemv_bf16 (new; the W4A16 decode, M <= 16 tokens): in bf16 x[M][K], in u8 w (repacked,
 // non-gated) [N][K/2], in u8 w_sf (repacked), out bf16 y[M][N], i32 M, launch i32 N, i32 K, i32 nb, i32 sb.
 // Grid N/16, block 256, dynamic LDS M*(sb*1024 + 16) + K/2 bytes: one 16-row group per workgroup. Wave w
 // takes the 128-wide k-tiles kt = 4i + w (equal shares; its scale is byte w of each scale dword of the
@@ -1807,7 +1807,7 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_bmm_fc1(
   CLOCK_PROBE_END(dbg);
 }
 
-// Dense e4m3-output mode of the FC1 family: c[t][n] = e4m3(acc * d_scale[0]).
+// Dense e4m3-output mode of the FC1 family (the prefill GEMM, one batch): c[t][n] = e4m3(acc * d_scale[0]).
 // a, sf_a, b [M][k], sf_b linear, c u8 [M][m], d_scale f32[1], i32 M; launch adds i32 m, i32 k, f32* dbg.
 // Grid [m/256, ceil(M/128), 1], block 512.
 extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_e4m3(const uint8_t* a, const uint8_t* sf_a,

@@ -1,4 +1,4 @@
-"""BASELINE config 5 on the GPU, through the C ABI, against the CPU oracle.
+"""Config 5 (the quantized layer stack) on the GPU, through the C ABI, against the CPU oracle.
 
 * The dense bf16-output GEMM (kern_mxfp4_gemm_bf16) at the stack's shapes: QKV [M, 7168] x [9216, 7168] and
   O [M, 8192] x [7168, 8192] at M = 64 and 2048, every row: the f32 accumulators within the north-star

@@ -40,7 +40,7 @@ def pack(fields):
     return out + b"\0" * (-len(out) % 8)
 
 
-# K3 (the reference's own shapes) and BASELINE config 4
+# K3 (the reference's own shapes) and config 4 (E = 256, top-8, H = 7168, I = 2048)
 SHAPES = [dict(H=3584, I=3072, E=224, k=16), dict(H=7168, I=2048, E=256, k=8)]
 
 
