@@ -76,10 +76,16 @@ def test_quant_bitexact(ops, oracle, T, K):
 
 # --------------------------------------------------------------------------------------- repack
 
-@pytest.mark.parametrize("gated", [0, 1])
-def test_repack_bitexact(ops, oracle, gated):
-    E, rows, K = 3, 64, 1024
-    w, sf = wl.mxfp4_weights(11 + gated, E, rows, K, 118, 136)
+# weight_prep repacks, bit for bit against the oracle: small experts, gated (FC1) and plain (FC2); the
+# smallest shapes the ops take (one 16-row group, K = 512; three row groups, K = 1536); and the real shapes,
+# several experts each: K3's FC1 (6144 gate/up rows, K = 3584) and FC2 (3584 rows, K = 3072), config 4's FC1
+# (4096 rows, K = 7168) and FC2 (7168 rows, K = 2048), and config 2's dense weights (18432 rows, K = 7168)
+@pytest.mark.parametrize("E,rows,K,gated", [(3, 64, 1024, 0), (3, 64, 1024, 1), (1, 16, 512, 1), (2, 48, 1536, 0),
+                                            (4, 6144, 3584, 1), (4, 3584, 3072, 0), (2, 4096, 7168, 1),
+                                            (2, 7168, 2048, 0), (1, 18432, 7168, 0)])
+def test_repack_bitexact(ops, oracle, E, rows, K, gated):
+    print(f"[repack] E={E} rows={rows} K={K} gated={gated}", flush=True)
+    w, sf = wl.mxfp4_weights(11 + gated + rows, E, rows, K, 118, 136)
     wd, sfd = ops.repack_weights(to_dev(w), to_dev(sf), gated=bool(gated))
     _sync()
     np.testing.assert_array_equal(to_np(wd).reshape(-1), oracle.w_shuffle(w, E, rows, K // 2, gated).reshape(-1))
