@@ -584,7 +584,9 @@ def test_mxfp8_gemm_kat(ops):
     np.testing.assert_array_equal(to_np(out), wl.f32_to_bf16_bits(mxfp8_kat(-1)["want"]))
 
 
-@pytest.mark.parametrize("m,n,k", [(300, 520, 1024), (64, 1000, 2080), (200, 256, 96), (2048, 2048, 7168)])
+# ragged m, n and k; and the benchmark's shape, config 3's 4096 x 2048 x 7168
+@pytest.mark.parametrize("m,n,k", [(300, 520, 1024), (64, 1000, 2080), (200, 256, 96), (2048, 2048, 7168),
+                                   (4096, 2048, 7168)])
 def test_mxfp8_gemm_random(ops, oracle, m, n, k):
     from kern_amd import ops as o
     rng = np.random.default_rng(m + n + k)
