@@ -492,6 +492,10 @@ extern "C" int kern_candidate_tile(const char* op, const char* var, const kern_c
           continue;
         }
         uint64_t x;
+        for (const char* end : {"min", "max"})
+          if (w->get(end) && !u64_of(w->get(end), x))
+            return kern_amd_fail(KERN_ERR_MANIFEST, "%s: launch `%s`: when.%s must be a non-negative integer",
+                                 pi.c_str(), entry.c_str(), end);
         if (u64_of(w->get("min"), x)) lo = has_lo ? std::max(lo, x) : x, has_lo = true;
         if (u64_of(w->get("max"), x)) hi = has_hi ? std::min(hi, x) : x, has_hi = true;
       }

@@ -141,6 +141,20 @@ def test_a_piece_conditioned_on_another_var_cannot_be_narrowed(lib):
         ops.candidate_tile("scale", "tokens", [(c, None, None)])
 
 
+def test_malformed_pieces_are_refused(lib):
+    c = candidate("m", 1, [launch("m", "k")])
+    c["ops"]["scale"]["impl"]["launches"][0]["when"] = {"var": "tokens", "min": -2}
+    with pytest.raises(ops.KernError, match="when.min must be a non-negative integer"):
+        ops.candidate_tile("scale", "tokens", [(c, None, None)])
+    with pytest.raises(ops.KernError, match="unknown field `programs`"):
+        ops.candidate_tile("scale", "tokens", [({"ops": {}, "programs": {}}, None, None)])
+    with pytest.raises(ops.KernError, match="a launch must be an object"):
+        ops.candidate_tile("scale", "tokens", [({"ops": {"scale": {"params": [], "impl": {"launches": [3]}}}},
+                                                None, None)])
+    with pytest.raises(ops.KernError, match="no launch of any piece runs"):
+        ops.candidate_tile("scale", "tokens", [])
+
+
 def test_pieces_without_the_op_or_with_other_params_are_refused(lib):
     a = candidate("m1", 1, [launch("m1", "k1")])
     b = candidate("m2", 2, [launch("m2", "k2")])
