@@ -286,8 +286,9 @@ int kern_moe_sf_shuffle(const void* raw, void* out, int32_t experts, int32_t row
  * in i32 topk_idx[tokens][topk] -> out counts[2*local_experts], cta_batch[ctas], cta_limit[ctas],
  * num_non_exiting[1], total_padded[1], route_map[ctas*128], exp2perm[tokens*topk].
  * ctas = local_experts + ceil(tokens*topk/128) bounds the slots. local_experts <= 512,
- * tokens*topk + 128*local_experts <= INT32_MAX (the padded rows are i32). One launch below 16384 expanded ids, else three (min(64, ceil(ids/4096))
- * workgroups; exp2perm holds per-chunk counts between them), all on `stream`. */
+ * tokens*topk + 128*local_experts <= INT32_MAX (the padded rows are i32). At tokens = 0 the tables still
+ * come out (no live slots) and topk_idx / exp2perm may be null. One launch below 16384 expanded ids, else
+ * three (min(64, ceil(ids/4096)) workgroups; exp2perm holds per-chunk counts between them), all on `stream`. */
 int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_t* cta_batch, int32_t* cta_limit,
                      int32_t* num_non_exiting, int32_t* total_padded, int32_t* route_map, int32_t* exp2perm,
                      int32_t tokens, int32_t topk, int32_t local_start, int32_t local_experts, void* stream);

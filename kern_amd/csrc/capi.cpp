@@ -399,8 +399,10 @@ extern "C" int kern_moe_routing(const int32_t* topk_idx, int32_t* counts, int32_
   REQUIRE(tokens >= 0 && topk > 0 && local_experts > 0 && local_experts <= 512 && local_start >= 0,
           "moe_routing: need tokens >= 0, topk > 0, 0 < local_experts <= 512 (got %d, %d, %d)", tokens, topk,
           local_experts);
-  REQUIRE(topk_idx && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm,
-          "moe_routing: null buffer");
+  // the tables are written at every token count (zero live slots for an empty batch); the ids and exp2perm
+  // are empty at zero tokens and may then be null
+  REQUIRE(counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map, "moe_routing: null buffer");
+  REQUIRE(tokens == 0 || (topk_idx && exp2perm), "moe_routing: null buffer");
   // expanded ids and padded rows (at most tokens * topk + 128 * local_experts) are i32 in the tables
   const int64_t n = (int64_t)tokens * topk;
   REQUIRE(n + 128LL * local_experts <= INT32_MAX,
@@ -425,9 +427,9 @@ extern "C" int kern_moe_quant_routing(const void* x, void* q, void* sf, int32_t 
           K, tokens);
   REQUIRE(topk > 0 && local_experts > 0 && local_experts <= 512 && local_start >= 0,
           "moe_quant_routing: need topk > 0, 0 < local_experts <= 512 (got %d, %d)", topk, local_experts);
-  REQUIRE(topk_idx && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm,
+  REQUIRE(counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map,
           "moe_quant_routing: null buffer");
-  REQUIRE(tokens == 0 || (x && q && sf), "moe_quant_routing: null buffer");
+  REQUIRE(tokens == 0 || (x && q && sf && topk_idx && exp2perm), "moe_quant_routing: null buffer");
   // quantizer workgroups of 1024 lanes (16 elements a lane); the routing block's LDS holds every workgroup
   // of the launch to one per CU, so the fused launch is taken when all of them fit in one round
   const int64_t qwg = ((int64_t)tokens * (K / 16) + 1023) / 1024;

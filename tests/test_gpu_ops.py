@@ -213,7 +213,7 @@ def test_gemm_e4m3_per_tensor(ops, oracle, M, m, k):
                                                     (2048, 256, 8, 0, 256, 0), (2049, 512, 8, 0, 512, 0),
                                                     (16384, 224, 16, 56, 56, 0), (65536, 256, 8, 0, 256, 0),
                                                     (4096, 64, 4, 0, 64, 1), (3000, 256, 8, 128, 64, 0),
-                                                    (4096, 8, 4, 3, 1, 0)])
+                                                    (4096, 8, 4, 3, 1, 0), (0, 256, 8, 0, 256, 0)])
 def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
     ids = wl.topk_ids(T * 31 + E, T, E, k)
     if skew:
@@ -243,7 +243,8 @@ def test_routing_bitexact(ops, oracle, T, E, k, start, local, skew):
 @pytest.mark.parametrize("T,E,k,start,local,K", [(1, 256, 8, 0, 256, 7168), (4, 256, 8, 0, 256, 7168),
                                                  (64, 256, 8, 0, 256, 7168), (512, 256, 8, 0, 256, 7168),
                                                  (300, 224, 16, 56, 56, 3584), (600, 256, 8, 0, 256, 7168),
-                                                 (2048, 256, 8, 0, 256, 7168), (3, 8, 2, 0, 8, 96)])
+                                                 (2048, 256, 8, 0, 256, 7168), (3, 8, 2, 0, 8, 96),
+                                                 (0, 256, 8, 0, 256, 7168)])
 def test_quant_routing_fused(ops, oracle, T, E, k, start, local, K):
     x = wl.activations_bf16(11 + T, T, K, outlier_frac=0.01)
     x[:min(T, 8)] = _special_rows(K)[:min(T, 8)]
