@@ -369,6 +369,45 @@ def test_fc2_live_count_is_capped_by_the_tables(ops, oracle):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
+def test_empty_batch_chain(ops):
+    """An empty batch through the MoE chain: zero tokens routed (the tables say no live slots), then FC1, FC2
+    and the finalize on those tables write nothing (every output keeps its sentinel bytes)."""
+    E, k, H, I = 8, 2, 1024, 512
+    ctas = ops.ctas_bound(0, k, E)
+    rows = ctas * 128
+    i32 = torch.int32
+    tab = {n: torch.full((sz,), -7, dtype=i32, device="cuda") for n, sz in
+           [("counts", 2 * E), ("cb", ctas), ("cl", ctas), ("nne", 1), ("tp", 1), ("rm", rows)]}
+    ops.moe_routing(torch.empty((0, k), dtype=i32, device="cuda"), tab["counts"], tab["cb"], tab["cl"], tab["nne"],
+                    tab["tp"], tab["rm"], torch.empty(0, dtype=i32, device="cuda"), tokens=0, topk=k, local_start=0,
+                    local_experts=E)
+    _sync()
+    assert (int(tab["nne"][0]), int(tab["tp"][0])) == (0, 0) and not tab["counts"].any()
+    w1, s1 = wl.mxfp4_weights(31, E, 2 * I, H, 118, 126)
+    w2, s2 = wl.mxfp4_weights(32, E, H, I, 118, 126)
+    w1p, s1p = ops.repack_weights(to_dev(w1), to_dev(s1), gated=True)
+    w2p, s2p = ops.repack_weights(to_dev(w2), to_dev(s2))
+    q = torch.zeros((1, H), dtype=torch.uint8, device="cuda")  # a token row the launches must not read
+    qs = torch.zeros((1, H // 32), dtype=torch.uint8, device="cuda")
+    c1 = torch.full((rows, I), 0x5A, dtype=torch.uint8, device="cuda")
+    sf1 = torch.full((ops.r128c4_bytes(rows, I // 32),), 0x5A, dtype=torch.uint8, device="cuda")
+    c2 = torch.full((rows, H), 0x5A5A, dtype=torch.int16, device="cuda").view(torch.bfloat16)
+    alpha = torch.full((E,), 4.0, device="cuda")
+    beta = torch.full((E,), 25.0, device="cuda")
+    ops.trtllm_bmm_mxe4m3_mxe2m1_mxe4m3(w1p, s1p, q, qs, c1, sf1, tab["rm"], alpha, beta, tab["nne"], tab["tp"],
+                                        tab["cb"], tab["cl"], m=2 * I, k=H, ctas=ctas)
+    ops.trtllm_bmm_bf16_mxe2m1_mxe4m3(w2p, s2p, c1, sf1, c2, tab["nne"], tab["tp"], tab["cb"], tab["cl"], m=H, k=I,
+                                      ctas=ctas, sf_b_r128c4=True)
+    y = torch.full((1, H), 0x5A5A, dtype=torch.int16, device="cuda").view(torch.bfloat16)
+    gamma = torch.ones(H, dtype=torch.bfloat16, device="cuda")
+    tw = torch.ones((1, k), dtype=torch.float32, device="cuda")
+    ops.moe_finalize_rms(c2, torch.zeros(k, dtype=i32, device="cuda"), tw, gamma, y, 0, H=H, topk=k, eps=1e-6)
+    _sync()
+    assert bool((c1 == 0x5A).all()) and bool((sf1 == 0x5A).all()), "fc1 wrote rows of an empty batch"
+    assert bool((c2.view(torch.int16) == 0x5A5A).all()), "fc2 wrote rows of an empty batch"
+    assert bool((y.view(torch.int16) == 0x5A5A).all()), "the finalize wrote a token of an empty batch"
+
+
 def _check_fc1(ops, oracle, ids, E, m, K, local_start=0, local=None):
     """FC1 through the C ABI over a routed batch, every live slot checked against the oracle (tests/_moe.py)."""
     from tests import _moe
