@@ -112,6 +112,28 @@ def test_graph_program_replays_new_inputs(ops, weights, rt):
     assert e.value.code == 4 and "captured at" in str(e.value)
 
 
+def test_programs_at_chunked_routing_sizes(ops, weights):
+    """From mf.ROUTE_CHUNKED_MIN expanded ids on, moe_routing's manifest launches are the chunked count / scan /
+    rank, whose grid is a clamp of the token count: the runtime picks them by `when` and sizes them per call,
+    launch by launch and inside graphs replayed with new inputs, and the layer stays bit-identical to the
+    direct op calls (which choose the same launches in the C ABI)."""
+    first = mf.ROUTE_CHUNKED_MIN // K
+    r = ops.Runtime(mf.moe_layer_manifest(H, I, E, K, first + 320, ops.code_object_sha256()))
+    try:
+        for name, data in weights.items():
+            r.load_weight(name, data)
+        r.derive()
+        for T, seed, program in [(first - 1, 501, "moe_layer"), (first, 503, "moe_layer"),
+                                 (first + 301, 505, "moe_layer"), (first + 301, 507, "moe_layer_graph"),
+                                 (first + 301, 509, "moe_layer_graph"), (first, 511, "moe_layer_graph")]:
+            print(f"[runtime] {program} T={T} (chunked routing from T={first})", flush=True)
+            x, ids, tw = _inputs(seed, T)
+            np.testing.assert_array_equal(_run(r, program, x, ids, tw), _direct(ops, weights, x, ids, tw),
+                                          err_msg=f"{program} T={T}")
+    finally:
+        r.close()
+
+
 def test_misuse(ops, rt):
     for call, code in [
         (lambda: rt.run("moe_layer", {"tokens": TMAX + 1}), 4),     # above the var's max
