@@ -1972,22 +1972,28 @@ extern "C" __global__ __launch_bounds__(512) void kern_mx_gemm_mxfp8(const uint8
     const int kr = K & 127;  // valid bytes of a partial last tile (its chunks past K are zeros)
     const bool vs = !last || kr == 0 || 32 * g < kr;  // this lane's k block lies within K
     // Scales (R128c4: row t's four k blocks are one dword at (t & 31) * 16 + ((t & 127) >> 5) * 4 of its
-    // 128-row block). The dwords of subtiles q and q + 2 (rows 32 apart) are neighbours, so one 8-byte read
-    // fetches both, and the lane takes its k block's byte by a shift. Lanes that differ only in their k block
-    // read the same 8 bytes. A read per byte cost the LDS as much as a 16-byte read, and conflicted.
+    // 128-row block). The 16 bytes at (t & 31) * 16 hold the dwords of rows t, t + 32, t + 64 and t + 96, so
+    // one 16-byte read per subtile pair fetches the dwords of subtiles q and q + 2 (the lane keeps the half
+    // of its 64-row group), and the lane takes its k block's byte by a shift. Lanes that differ only in their
+    // k block read the same 16 bytes, and each group of 16 lanes reads 256 contiguous bytes: no bank
+    // conflicts. (Two 8-byte reads, which the compiler paired into one ds_read2_b64 of two rows 256 bytes
+    // apart, put both halves of every lane on the same banks: a sixth of the LDS cycles were conflicts.
+    // A read per byte cost the LDS as much as a 16-byte read, and conflicted too.)
     const int sh = 8 * g;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const uint2 d = *reinterpret_cast<const uint2*>(sc + 512 + (wn >> 1) * 512 + (q * 16 + cl) * 16 + 8 * (wn & 1));
-      sw_[q] = vs ? (d.x >> sh) & 255u : 127u;
-      sw_[q + 2] = vs ? (d.y >> sh) & 255u : 127u;
+      const v4u d = *reinterpret_cast<const v4u*>(sc + 512 + (wn >> 1) * 512 + (q * 16 + cl) * 16);
+      const uint32_t lo = (wn & 1) ? d[2] : d[0], hi = (wn & 1) ? d[3] : d[1];
+      sw_[q] = vs ? (lo >> sh) & 255u : 127u;
+      sw_[q + 2] = vs ? (hi >> sh) & 255u : 127u;
     }
     uint32_t sa4[2][2];  // [half][subtile]: rows wm*64 + (2h + q)*16 + cl
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const uint2 d = *reinterpret_cast<const uint2*>(sc + (q * 16 + cl) * 16 + 8 * wm);
-      sa4[0][q] = vs ? (d.x >> sh) & 255u : 127u;
-      sa4[1][q] = vs ? (d.y >> sh) & 255u : 127u;
+      const v4u d = *reinterpret_cast<const v4u*>(sc + (q * 16 + cl) * 16);
+      const uint32_t lo = wm ? d[2] : d[0], hi = wm ? d[3] : d[1];
+      sa4[0][q] = vs ? (lo >> sh) & 255u : 127u;
+      sa4[1][q] = vs ? (hi >> sh) & 255u : 127u;
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
