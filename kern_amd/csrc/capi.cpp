@@ -619,7 +619,9 @@ extern "C" int kern_moe_finalize_rms(const void* fc2_out, const int32_t* exp2per
   Args a;
   a.put(fc2_out), a.put(exp2perm), a.put(topk_weight), a.put(gamma), a.put(out), a.put(tokens), a.put(H);
   a.put(topk), a.put(eps);
-  return launch("kern_mx_moe_finalize_rms", (uint32_t)tokens, 1, 1, 256, stream, a);
+  // one thread per 8-column chunk of the row, in whole waves (at most 1024 threads: H <= 8192)
+  const uint32_t block = (uint32_t)(((H >> 3) + 63) / 64 * 64);
+  return launch("kern_mx_moe_finalize_rms", (uint32_t)tokens, 1, 1, block, stream, a);
 }
 
 extern "C" int kern_moe_finalize(const void* fc2_out, const int32_t* exp2perm, const float* topk_weight, void* out,

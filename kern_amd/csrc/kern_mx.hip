@@ -2481,44 +2481,39 @@ KERN_DEV v4u bf16x8(const float v[8]) {
 
 // op moe_finalize_rms (head.json, call l1.finalize): in bf16 fc2_out [padded][H], in i32 exp2perm [T*topk],
 // in f32 topk_weight [T][topk], in bf16 gamma [H], out bf16 out [T][H], i32 T; launch adds i32 H, i32 topk,
-// f32 eps. Grid [T], block 256.
-extern "C" __global__ __launch_bounds__(256) void kern_mx_moe_finalize_rms(
+// f32 eps. Grid [T], block = the row's H/8 chunks rounded up to a multiple of 64 (at most 1024: H <= 8192):
+// one chunk per thread, whose eight routed rows are in flight together. A token's whole row in one pass of
+// small threads: at config 4's T = 512 and at T = 2048 this ran 6% shorter than 256 threads of four chunks
+// each (185 registers a thread allowed two such workgroups per CU, 52 allow the CU's share of the token rows).
+extern "C" __global__ __launch_bounds__(1024) void kern_mx_moe_finalize_rms(
     const uint16_t* __restrict__ fc2_out, const int* __restrict__ exp2perm, const float* __restrict__ topk_w,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int T, int H, int topk, float eps) {
-  __shared__ float red[4];
+  __shared__ float red[16];
   (void)T;
-  const int t = blockIdx.x, tid = threadIdx.x, chunks = H >> 3;
-  constexpr int Q = 4;  // chunks per thread kept in registers between the passes (H <= 8192)
-  // gamma's chunks first: their loads overlap the routed rows' instead of following the reduction
-  v4u gm[Q];
-#pragma unroll
-  for (int q = 0; q < Q; ++q)
-    gm[q] = tid + 256 * q < chunks ? *reinterpret_cast<const v4u*>(gamma + (tid + 256 * q) * 8) : (v4u){0, 0, 0, 0};
-  float y[Q][8];
+  const int t = blockIdx.x, tid = threadIdx.x, chunks = H >> 3, nw = blockDim.x >> 6;
+  const bool live = tid < chunks;
+  // gamma's chunk first: its load overlaps the routed rows' instead of following the reduction
+  const v4u gm = live ? *reinterpret_cast<const v4u*>(gamma + tid * 8) : (v4u){0, 0, 0, 0};
+  float y[1][8];
+  moe_combine_chunks<1>(fc2_out, exp2perm, topk_w, t, H, topk, tid, chunks, y);
   float ss = 0.f;
-  moe_combine_chunks<Q>(fc2_out, exp2perm, topk_w, t, H, topk, tid, chunks, y);
+  if (live) {
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    if (tid + 256 * q < chunks) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[q][e], y[q][e], ss);
-    }
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[0][e], y[0][e], ss);
   }
-  // sum of squares over the row: wave reduction, then the four waves in LDS
+  // sum of squares over the row: wave reduction, then the waves in LDS, in wave order
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  const float r = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
+  float tot = 0.f;
+  for (int w = 0; w < nw; ++w) tot += red[w];
+  const float r = 1.0f / sqrtf(tot / (float)H + eps);
+  if (live) {
+    float v[8];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int c = tid + 256 * q;
-    if (c < chunks) {
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = y[q][e] * r * bf16_bits_to_f32((gm[q][e >> 1] >> (16 * (e & 1))) & 0xffffu);
-      *reinterpret_cast<v4u*>(out + (int64_t)t * H + c * 8) = bf16x8(v);
-    }
+    for (int e = 0; e < 8; ++e) v[e] = y[0][e] * r * bf16_bits_to_f32((gm[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+    *reinterpret_cast<v4u*>(out + (int64_t)t * H + tid * 8) = bf16x8(v);
   }
 }
 

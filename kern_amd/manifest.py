@@ -155,7 +155,8 @@ def moe_fc2(m: int, k: int, experts: int, topk: int) -> dict:
 
 def moe_finalize_rms(H: int, topk: int, eps: float = 1e-6) -> dict:
     """moe_finalize_rms(in bf16 fc2_out, in i32 exp2perm, in f32 topk_weight, in bf16 gamma, out bf16 out,
-    i32 T); launch adds i32 H, i32 topk and f32 eps. One workgroup per token (grid.x = tokens)."""
+    i32 T); launch adds i32 H, i32 topk and f32 eps. One workgroup per token (grid.x = tokens) of one thread
+    per 8-column chunk of the row, in whole waves (the block kern_moe_finalize_rms launches)."""
     assert H % 8 == 0 and H <= 8192
     p = ["in buffer<bf16>", "in buffer<i32>", "in buffer<f32>", "in buffer<bf16>", "out buffer<bf16>", "i32"]
     return {
@@ -163,7 +164,7 @@ def moe_finalize_rms(H: int, topk: int, eps: float = 1e-6) -> dict:
         "impl": {"launches": [{
             "module": MODULE, "entry": "kern_mx_moe_finalize_rms",
             "params": p + ["i32", "i32", "f32"],
-            "block": [256, 1, 1],
+            "block": [_ceil(H // 8, 64) * 64, 1, 1],
             "grid": [{"mul": ["tokens", 1]}, 1, 1],
             "args": [{"param": i} for i in range(6)] + [{"i32": H}, {"i32": topk}, {"f32": eps}],
         }]},

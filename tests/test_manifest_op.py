@@ -113,7 +113,7 @@ def test_plan_grids_and_kernargs(lib, shape, T):
                                                                             ("q", 0)])
 
     p = ops.op_plan(o["moe_finalize_rms"], 0, bufs(5) + [T], v)
-    assert p["grid"] == (T, 1, 1) and p["block"] == (256, 1, 1)
+    assert p["grid"] == (T, 1, 1) and p["block"] == (-(-H // 8 // 64) * 64, 1, 1)
     assert p["args"] == pack([("Q", 0x1000 * (i + 1)) for i in range(5)] + [("i", T), ("i", H), ("i", k), ("f", 1e-6)])
 
     for name, rows, rb, gated in [("k3_moe_w_shuffle", 2 * I, H // 2, 1), ("k3_moe_sf_shuffle", H, I // 32, 0)]:
