@@ -2485,21 +2485,33 @@ KERN_DEV v4u bf16x8(const float v[8]) {
 // one chunk per thread, whose eight routed rows are in flight together. A token's whole row in one pass of
 // small threads: at config 4's T = 512 and at T = 2048 this ran 6% shorter than 256 threads of four chunks
 // each (185 registers a thread allowed two such workgroups per CU, 52 allow the CU's share of the token rows).
+// A launch with fewer threads (any multiple of 64) is still correct: its threads take chunks tid,
+// tid + blockDim, .. twice, once for the row's sum of squares and once for the output, reading the routed
+// rows twice.
 extern "C" __global__ __launch_bounds__(1024) void kern_mx_moe_finalize_rms(
     const uint16_t* __restrict__ fc2_out, const int* __restrict__ exp2perm, const float* __restrict__ topk_w,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int T, int H, int topk, float eps) {
   __shared__ float red[16];
   (void)T;
-  const int t = blockIdx.x, tid = threadIdx.x, chunks = H >> 3, nw = blockDim.x >> 6;
+  const int t = blockIdx.x, tid = threadIdx.x, chunks = H >> 3, nt = blockDim.x, nw = nt >> 6;
+  const bool whole = chunks <= nt;  // one chunk per thread at most (uniform)
   const bool live = tid < chunks;
   // gamma's chunk first: its load overlaps the routed rows' instead of following the reduction
-  const v4u gm = live ? *reinterpret_cast<const v4u*>(gamma + tid * 8) : (v4u){0, 0, 0, 0};
+  const v4u gm = whole && live ? *reinterpret_cast<const v4u*>(gamma + tid * 8) : (v4u){0, 0, 0, 0};
   float y[1][8];
-  moe_combine_chunks<1>(fc2_out, exp2perm, topk_w, t, H, topk, tid, chunks, y);
   float ss = 0.f;
-  if (live) {
+  if (whole) {
+    moe_combine_chunks<1>(fc2_out, exp2perm, topk_w, t, H, topk, tid, chunks, y);
+    if (live) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[0][e], y[0][e], ss);
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[0][e], y[0][e], ss);
+    }
+  } else {
+    for (int c = tid; c < chunks; c += nt) {
+      moe_combine_chunks<1>(fc2_out, exp2perm, topk_w, t, H, topk, c, chunks, y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[0][e], y[0][e], ss);
+    }
   }
   // sum of squares over the row: wave reduction, then the waves in LDS, in wave order
 #pragma unroll
@@ -2509,11 +2521,19 @@ extern "C" __global__ __launch_bounds__(1024) void kern_mx_moe_finalize_rms(
   float tot = 0.f;
   for (int w = 0; w < nw; ++w) tot += red[w];
   const float r = 1.0f / sqrtf(tot / (float)H + eps);
-  if (live) {
+  auto put = [&](int c, const v4u& g) {
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = y[0][e] * r * bf16_bits_to_f32((gm[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-    *reinterpret_cast<v4u*>(out + (int64_t)t * H + tid * 8) = bf16x8(v);
+    for (int e = 0; e < 8; ++e) v[e] = y[0][e] * r * bf16_bits_to_f32((g[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+    *reinterpret_cast<v4u*>(out + (int64_t)t * H + c * 8) = bf16x8(v);
+  };
+  if (whole) {
+    if (live) put(tid, gm);
+  } else {
+    for (int c = tid; c < chunks; c += nt) {
+      moe_combine_chunks<1>(fc2_out, exp2perm, topk_w, t, H, topk, c, chunks, y);
+      put(c, *reinterpret_cast<const v4u*>(gamma + c * 8));
+    }
   }
 }
 

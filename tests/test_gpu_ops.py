@@ -543,6 +543,24 @@ def test_moe_finalize_rms(ops, oracle, T, H, k):
     assert _ulp(to_np(out).view(np.uint16), ref).max() <= 1
 
 
+@pytest.mark.parametrize("T,H,k,block", [(9, 7168, 8, 256), (5, 3584, 16, 64), (4, 8192, 2, 512), (3, 512, 4, 1024)])
+def test_moe_finalize_rms_any_block(ops, oracle, T, H, k, block):
+    """A manifest may launch the kernel with another whole-wave block than the C ABI's (H/8 threads rounded up
+    to 64): with fewer threads than chunks each thread takes several, with more the extra ones idle."""
+    from kern_amd import manifest as mf
+    print(f"[finalize_rms] T={T} H={H} k={k} block {block}", flush=True)
+    rows = ((T * k + 127) // 128 + 4) * 128
+    fc2, e2p, w = _finalize_case(T, H, k, rows, 60 + H)
+    gamma = wl.f32_to_bf16_bits((np.random.default_rng(H + 1).random(H) + 0.5).astype(np.float32))
+    op = mf.moe_finalize_rms(H, k)
+    op["impl"]["launches"][0]["block"] = [block, 1, 1]
+    out = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
+    ops.ManifestOp(op)(to_dev(fc2), to_dev(e2p), to_dev(w), to_dev(gamma), out, T, vars={"tokens": T})
+    _sync()
+    ref = oracle.moe_finalize(fc2, e2p, w, gamma, T, H, k, 1e-6)
+    assert _ulp(to_np(out).view(np.uint16), ref).max() <= 1
+
+
 # --------------------------------------------------------------------------------------- weight_prep
 
 def test_weight_p1_and_cast(ops):
