@@ -105,6 +105,21 @@ _NZ = ctypes.c_void_p(16)  # a non-null address that no call here dereferences (
     (lambda L: L.kern_moe_routing(*([_NZ] * 8), 1 << 28, 16, 0, 8, None), "past the i32 tables"),
     (lambda L: L.kern_moe_routing(*([_NZ] * 8), (2**31 - 1 - 128 * 512) // 8 + 1, 8, 0, 512, None), "past the i32 tables"),
     (lambda L: L.kern_fill_random_u8(None, 16, 1, 0, 0, None), "span"),
+    (lambda L: L.kern_moe_quant_routing(None, None, None, 4, 7168, *([None] * 8), 8, 0, 513, None),
+     "0 < local_experts <= 512"),
+    (lambda L: L.kern_moe_quant_routing(None, None, None, 4, 7000, *([None] * 8), 8, 0, 64, None), "K % 32"),
+    (lambda L: L.kern_moe_finalize_rms(*([None] * 5), 4, 8200, 8, 1e-6, None), "0 < H <= 8192"),
+    (lambda L: L.kern_moe_finalize_rms(*([None] * 5), 4, 7168, 8, -1.0, None), "eps >= 0"),
+    (lambda L: L.kern_moe_finalize_rms(*([None] * 5), 4, 7168, 8, 1e-6, None), "null buffer"),
+    (lambda L: L.kern_moe_finalize(*([None] * 4), 4, 100, 8, None), "H % 8 == 0"),
+    (lambda L: L.kern_mxfp8_quant_f32(None, None, None, 4, 33, None), "K % 32"),
+    (lambda L: L.kern_mxfp8_gemm_bf16(*([None] * 5), 16, 16, 48, 16, None), "k % 32 == 0"),
+    (lambda L: L.kern_mxfp8_gemm_bf16(*([None] * 5), 16, 32, 64, 16, None), "ldc >= n"),
+    (lambda L: L.kern_mxfp8_gemm_bf16(*([_NZ] * 5), 16, 16, 0, 16, None), "k == 0 leaves c undefined"),
+    (lambda L: L.kern_silu_mul(None, None, 4, 12, None), "d % 8 == 0"),
+    (lambda L: L.kern_rope_table_bf16(None, None, 4, 2048, 4096, 10000.0, None), "0 < half <= 1024"),
+    (lambda L: L.kern_iota_i32(None, 4, 0, 1, 0, None), "stride >= 1"),
+    (lambda L: L.kern_fill_f32(None, 4, 1.0, None), "a buffer"),
     # the LDS ring addresses activations by 32-bit offsets from the buffer's base: past 4 GiB is refused
     (lambda L: L.kern_trtllm_bmm_bf16_mxe2m1_mxe4m3(*([_NZ] * 9), 256, 8192, 4200, 1, None, None), "below 4 GiB"),
     (lambda L: L.kern_mxfp4_gemm_e4m3(*([_NZ] * 6), 1 << 20, 256, 8192, None, None), "below 4 GiB"),
