@@ -16,6 +16,8 @@ struct-taking kernels (types.rs:1193-1260).
 """
 from __future__ import annotations
 
+import json
+
 MODULE = "kern_mx"
 BMM_THREADS = 512  # threads of one GEMM workgroup (8 waves)
 MOE_WORKGROUPS = 256  # the MoE GEMMs are persistent: one workgroup per CU
@@ -188,6 +190,131 @@ def cublaslt_mxfp8_tn(n: int, rows_var: str = "tokens") -> dict:
             "args": [{"param": i} for i in range(8)] + [{"i32": n}],
         }]},
     }
+
+
+# The dense ops beside the MoE path, whose entry points choose a kernel by row count in host code
+# (kern_mxfp4_gemv_bf16, kern_mxfp4_gemm_bf16, kern_moe_quant_routing), as manifest ops: the same choices as
+# launches conditioned on the rows var by `when`, so that a manifest, and candidate tiling, sees them. The
+# rows (M, tokens) reach the kernels from the var, as a 4-byte pack, so that the dynamic LDS sized from the
+# var always matches the kernel's own count. The reference has no such ops (its dense MX GEMM is the
+# runtime's built-in `extern:cublaslt_mxfp8_tn`).
+GEMV_FIXED_NKT = (2, 4, 8, 14, 16)  # K / 512 with an unrolled kern_mx_gemv_bf16_r{K/512}
+WALK_KTW = (1, 2, 4, 7, 8)          # K / 1024 with a persistent kern_mx_gemv_bf16_p* / kern_mx_gemm_bf16_s*
+GEMV_MAX_ROWS = 16
+
+
+def _rows(rows_var: str) -> dict:
+    return {"pack": {"size": 4, "fields": [{"at": 0, "var": rows_var}]}}
+
+
+def _gemv_launch(N: int, K: int, M: int, rows_var: str) -> dict:
+    """The launch kern_mxfp4_gemv_bf16 makes for M rows of x [M][K] against weights [N][K/2] (capi.cpp)."""
+    kg = K // 512
+    params = ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>", "bytes<4>", "i32", "i32"]
+    args = [{"param": i} for i in range(4)] + [_rows(rows_var), {"i32": N}, {"i32": K}]
+    row_groups = [N // 16, 1, 1]
+    if kg in GEMV_FIXED_NKT and 2 * M * K <= 144 * 1024 and (M <= 3 or N <= 8192):
+        # one workgroup per 16-row group, each wave's x slice (2 * M * K bytes in all) in LDS
+        return {"entry": f"kern_mx_gemv_bf16_r{kg}", "params": params, "block": [256, 1, 1], "grid": row_groups,
+                "shared_mem": {"mul": [rows_var, 2 * K]}, "args": args}
+    if M <= 2:
+        gmax = _ceil(kg, 4)
+        return {"entry": "kern_mx_gemv_bf16_rg", "params": params + ["i32"], "block": [256, 1, 1],
+                "grid": row_groups, "shared_mem": {"mul": [rows_var, 4 * gmax * 1024]},
+                "args": args + [{"i32": gmax}]}
+    if K % 1024 == 0 and K // 1024 in WALK_KTW:
+        H = N // 8
+        hb = min(9, _ceil(H, 256))
+        return {"entry": f"kern_mx_gemv_bf16_p{K // 1024}", "params": params + ["i32"], "block": [512, 1, 1],
+                "grid": [_ceil(H, hb), 1, 1], "args": args + [{"i32": hb}]}
+    # any other shape: x staged in slices of sb k-tiles per wave, nb k-tiles of weights in flight together
+    sb = next(c for c in range(min(kg, GEMV_MAX_ROWS // M), 0, -1) if kg % c == 0)
+    nb = next((c for c in (7, 4, 2) if sb % c == 0), 1)
+    return {"entry": "kern_mx_gemv_bf16", "params": params + ["i32", "i32"], "block": [256, 1, 1],
+            "grid": row_groups, "shared_mem": M * (sb * 1024 + 16) + kg * 256, "args": args + [{"i32": nb}, {"i32": sb}]}
+
+
+def _by_rows(launch_at, rows_var: str, lo: int, hi: int) -> list:
+    """Launches for rows lo..hi: launch_at(M) at each M, runs of equal launches merged into one `when` range
+    (a lower end of 1 and an upper end of `None` bound nothing)."""
+    out = []
+    for M in range(lo, hi + 1):
+        L = {"module": MODULE, **launch_at(M)}
+        if out and json.dumps({k: v for k, v in out[-1].items() if k != "when"}, sort_keys=True) == \
+                json.dumps(L, sort_keys=True):
+            out[-1]["when"]["max"] = M
+        else:
+            out.append({**L, "when": {"var": rows_var, "min": M, "max": M}})
+    return out
+
+
+def mxfp4_gemv_bf16(N: int, K: int, rows_var: str = "tokens") -> dict:
+    """The W4A16 decode GEMV (C ABI kern_mxfp4_gemv_bf16): in bf16 x [M][K], in u8 w [N][K/2] and w_sf
+    (repacked), out bf16 y [M][N]; M = the value of `rows_var`, 1..16 (no launch runs past 16). One launch
+    per run of M that takes the same kernel: the unrolled row-group kernel while its x slices fit, the
+    persistent walk above, as the C ABI chooses."""
+    assert N % 16 == 0 and K % 512 == 0 and K <= 16384
+    return {"params": ["in buffer<bf16>", "in buffer<u8>", "in buffer<u8>", "out buffer<bf16>"],
+            "impl": {"launches": _by_rows(lambda M: _gemv_launch(N, K, M, rows_var), rows_var, 1, GEMV_MAX_ROWS)}}
+
+
+def mxfp4_gemm_bf16(N: int, K: int, rows_var: str = "tokens") -> dict:
+    """The dense MXFP4 x MXFP8 GEMM with bf16 out (C ABI kern_mxfp4_gemm_bf16): in u8 a [N][K/2], sf_a (the
+    repacked weights), b [M][K] and sf_b (MXFP8 activations, linear scales), out bf16 c [M][N]; M = the value
+    of `rows_var`. Up to 64 rows the persistent walk over the weights (K = 1024 * {1, 2, 4, 7, 8}), else
+    the tiled GEMM, grid [N/256, ceil(M/128)]; both with a null f32 debug pointer."""
+    assert N % 256 == 0 and K % 512 == 0
+    p = ["in buffer<u8>"] * 4 + ["out buffer<bf16>"]
+    tiled = {"module": MODULE, "entry": "kern_mx_gemm_bf16", "params": p + ["bytes<4>", "i32", "i32", "i64"],
+             "block": [BMM_THREADS, 1, 1], "grid": [N // 256, {"ceil_div": [rows_var, 128]}, 1],
+             "args": [{"param": i} for i in range(5)] + [_rows(rows_var), {"i32": N}, {"i32": K}, {"i64": 0}]}
+    if not (K % 1024 == 0 and K // 1024 in WALK_KTW):
+        return {"params": p, "impl": {"launches": [tiled]}}
+    H = N // 8
+    hb = min(9, _ceil(H, 256))
+    walk = {"module": MODULE, "entry": f"kern_mx_gemm_bf16_s{K // 1024}",
+            "params": p + ["i64", "bytes<4>", "i32", "i32", "i32"], "block": [512, 1, 1], "grid": [_ceil(H, hb), 1, 1],
+            "when": {"var": rows_var, "max": 64},
+            "args": [{"param": i} for i in range(5)] + [{"i64": 0}, _rows(rows_var), {"i32": N}, {"i32": K},
+                                                        {"i32": hb}]}
+    return {"params": p, "impl": {"launches": [walk, {**tiled, "when": {"var": rows_var, "min": 65}}]}}
+
+
+QUANT_ROUTING_WORKGROUPS = 255  # quantizer workgroups the fused launch holds (one round beside the routing block)
+
+
+def moe_quant_routing(K: int, topk: int, local_start: int, local_experts: int) -> dict:
+    """moe_quant and moe_routing in one op (C ABI kern_moe_quant_routing): in bf16 x [T][K], out u8 q, sf,
+    in i32 topk_idx, out the seven routing tables; T = the var `tokens`. While the quantizer's workgroups
+    (T * K/16 elements / 1024 lanes) fit in one round beside the routing workgroup, one launch does both
+    (kern_mx_quant_routing); past that, moe_routing's launches and then moe_quant's, as the C ABI does.
+    Bit for bit the outputs of the two ops."""
+    assert K % 32 == 0
+    fused_max = (QUANT_ROUTING_WORKGROUPS * 1024) // (K // 16)  # the most tokens with qwg <= 255
+    qwg = {"ceil_div": [{"mul": ["tokens", K // 16]}, 1024]}
+    rbufs = [{"param": i} for i in range(3, 11)]  # topk_idx and the seven tables: moe_routing's eight params
+    fused = {"module": MODULE, "entry": "kern_mx_quant_routing",
+             "params": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "i32", "in buffer<i32>"] +
+                       ["out buffer<i32>"] * 7 + ["bytes<4>", "i32", "i32", "i32"],
+             "block": [1024, 1, 1], "grid": [{"add": [qwg, 1]}, 1, 1],
+             "when": {"var": "tokens", "max": fused_max},
+             "args": [{"param": 0}, {"param": 1}, {"param": 2}, {"i32": K}] + rbufs +
+                     [_rows("tokens"), {"i32": topk}, {"i32": local_start}, {"i32": local_experts}]}
+    past = {"var": "tokens", "min": fused_max + 1}
+    routing = moe_routing(topk, local_start, local_experts)["impl"]["launches"]
+    quant = moe_quant(K)["impl"]["launches"][0]
+    split = []
+    for L in routing:  # each routing launch, its own `when` narrowed to the tokens past the fused launch
+        w = dict(L.get("when", {"var": "tokens"}))
+        w["min"] = max(w.get("min", 0), past["min"])
+        if "max" in w and w["max"] < w["min"]:
+            continue
+        split.append({**L, "args": [rbufs[i] if "param" in a else a for i, a in enumerate(L["args"])], "when": w})
+    q = {**quant, "when": past, "args": [{"param": 0}, {"param": 1}, {"param": 2}, _rows("tokens"), {"i32": K}],
+         "params": quant["params"][:3] + ["bytes<4>", "i32"]}
+    return {"params": ["in buffer<bf16>", "out buffer<u8>", "out buffer<u8>", "in buffer<i32>"] +
+                      ["out buffer<i32>"] * 7,
+            "impl": {"launches": [fused] + split + [q]}}
 
 
 def _fill(entry: str, params: list, launch_params: list, args: list, n: int) -> dict:

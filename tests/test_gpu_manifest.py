@@ -172,3 +172,66 @@ def test_mxfp8_kat_through_manifest_op(ops):
     op(*(_dev(c[x]) for x in ("a", "w")), out, *(_dev(c[x]) for x in ("a_sf", "w_sf")), M, N, K, vars={"tokens": M})
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), wl.f32_to_bf16_bits(c["want"]))
+
+
+# The dense ops whose C-ABI entries choose a kernel by row count: their manifest ops (launches conditioned on
+# `tokens` by `when`) against the C ABI, bit for bit, at row counts on either side of every switch.
+
+@pytest.mark.parametrize("N,K,Ms", [(18432, 7168, [1, 3, 4, 16]), (7168, 8192, [9, 10]), (2048, 3584, [1, 2, 3, 7, 16]),
+                                    (512, 1024, [1, 16])])
+def test_gemv_op_takes_the_c_abi_kernels(ops, N, K, Ms):
+    op = ops.ManifestOp(mf.mxfp4_gemv_bf16(N, K))
+    w, sf = wl.mxfp4_weights(300 + K, 1, N, K, 122, 132)
+    wp, sfp = ops.repack_weights(_dev(w[0]), _dev(sf[0]))
+    for M in Ms:
+        print(f"[manifest] mxfp4_gemv_bf16 N={N} K={K} M={M}", flush=True)
+        x = _dev(wl.activations_bf16(310 + M, M, K))
+        y0 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        y1 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        ops.mxfp4_gemv_bf16(x, wp, sfp, y0, M, N=N, K=K)
+        op(x, wp, sfp, y1, vars={"tokens": M})
+        torch.cuda.synchronize()
+        assert torch.equal(y0.view(torch.int16), y1.view(torch.int16)), M
+
+
+@pytest.mark.parametrize("N,K,Ms", [(9216, 7168, [17, 64, 65, 200]), (2048, 3584, [5, 130])])
+def test_dense_gemm_op_takes_the_c_abi_kernels(ops, N, K, Ms):
+    op = ops.ManifestOp(mf.mxfp4_gemm_bf16(N, K))
+    w, sf = wl.mxfp4_weights(320 + K, 1, N, K, 122, 132)
+    wp, sfp = ops.repack_weights(_dev(w[0]), _dev(sf[0]))
+    for M in Ms:
+        print(f"[manifest] mxfp4_gemm_bf16 N={N} K={K} M={M}", flush=True)
+        x = _dev(wl.activations_bf16(330 + M, M, K))
+        q = torch.zeros((M, K), dtype=torch.uint8, device="cuda")
+        qs = torch.zeros((M, K // 32), dtype=torch.uint8, device="cuda")
+        ops.moe_quant(x, q, qs, M, K=K)
+        c0 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        c1 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        ops.mxfp4_gemm_bf16(wp, sfp, q, qs, c0, M=M, m=N, k=K)
+        op(wp, sfp, q, qs, c1, vars={"tokens": M})
+        torch.cuda.synchronize()
+        assert torch.equal(c0.view(torch.int16), c1.view(torch.int16)), M
+
+
+@pytest.mark.parametrize("K,k,E,Ts", [(7168, 8, 256, [1, 582, 583, 2048]), (512, 16, 64, [8160, 8161])])
+def test_quant_routing_op_takes_the_c_abi_launches(ops, K, k, E, Ts):
+    op = ops.ManifestOp(mf.moe_quant_routing(K, k, 0, E))
+    for T in Ts:
+        print(f"[manifest] moe_quant_routing K={K} top-{k} E={E} T={T}", flush=True)
+        x = _dev(wl.activations_bf16(340 + T, T, K))
+        ids = _dev(wl.topk_ids(341 + T, T, E, k))
+        ctas = ops.ctas_bound(T, k, E)
+        outs = []
+        for path in ("c_abi", "manifest"):
+            q = torch.full((T, K), 0x5A, dtype=torch.uint8, device="cuda")
+            qs = torch.full((T, K // 32), 0x5A, dtype=torch.uint8, device="cuda")
+            tabs = [torch.full((n,), -7, dtype=torch.int32, device="cuda")
+                    for n in (2 * E, ctas, ctas, 1, 1, ctas * 128, T * k)]
+            if path == "c_abi":
+                ops.moe_quant_routing(x, q, qs, ids, *tabs, tokens=T, K=K, topk=k, local_start=0, local_experts=E)
+            else:
+                op(x, q, qs, ids, *tabs, vars={"tokens": T})
+            torch.cuda.synchronize()
+            outs.append([q, qs] + tabs)
+        for a, b in zip(*outs):
+            assert torch.equal(a, b), T

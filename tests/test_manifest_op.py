@@ -238,3 +238,55 @@ def test_ring_activations_past_4gib_are_refused(lib):
         ops.op_plan(o["moe_fc2"], 0, params, {"tokens": 258048})
     assert "4 GiB" in str(e.value)
     ops.op_plan(o["moe_fc2"], 0, params, {"tokens": 258047 - 15})
+
+
+def _runs(op, nparams, v):
+    """(entry, plan) of each launch of op that runs at vars v."""
+    out = []
+    for i, L in enumerate(op["impl"]["launches"]):
+        p = ops.op_plan(op, i, [0x1000 * (j + 1) for j in range(nparams)], v)
+        if not p["skip"]:
+            out.append((L["entry"], p))
+    return out
+
+
+@pytest.mark.parametrize("N,K", [(18432, 7168), (7168, 8192), (2048, 3584), (512, 1024), (1040, 16384)])
+def test_gemv_op_plans_one_launch_per_row_count(lib, N, K):
+    """The GEMV op's launches tile rows 1..16: at each M exactly one runs, its dynamic LDS fits gfx950's
+    160 KiB, and the kernel's M (after the four buffers) is the var's value; past 16 none runs."""
+    op = mf.mxfp4_gemv_bf16(N, K)
+    for M in range(1, 18):
+        r = _runs(op, 4, {"tokens": M})
+        if M > mf.GEMV_MAX_ROWS:
+            assert r == [], M
+            continue
+        assert len(r) == 1, (M, [e for e, _ in r])
+        entry, p = r[0]
+        assert entry.startswith("kern_mx_gemv_bf16") and p["shared"] <= 163840, (M, entry, p["shared"])
+        assert struct.unpack_from("<i", p["args"], 32)[0] == M and struct.unpack_from("<ii", p["args"], 36) == (N, K)
+
+
+def test_dense_gemm_op_plans(lib):
+    op = mf.mxfp4_gemm_bf16(9216, 7168)
+    for M, entry, m_at in [(1, "kern_mx_gemm_bf16_s7", 48), (64, "kern_mx_gemm_bf16_s7", 48),
+                           (65, "kern_mx_gemm_bf16", 40), (4096, "kern_mx_gemm_bf16", 40)]:
+        (e, p), = _runs(op, 5, {"tokens": M})
+        assert e == entry and struct.unpack_from("<i", p["args"], m_at)[0] == M, M
+        if e == "kern_mx_gemm_bf16":
+            assert p["grid"] == (9216 // 256, -(-M // 128), 1)
+    (e, _), = _runs(mf.mxfp4_gemm_bf16(2048, 3584), 5, {"tokens": 8})  # K = 3584: no walk instance
+    assert e == "kern_mx_gemm_bf16"
+
+
+def test_quant_routing_op_plans(lib):
+    """One launch while the quantizer's workgroups fit beside the routing workgroup, then moe_routing's
+    launches and moe_quant's, each with its own grid at that token count."""
+    K, k = 7168, 8
+    op = mf.moe_quant_routing(K, k, 0, 256)
+    fused_max = 255 * 1024 // (K // 16)
+    (e, p), = _runs(op, 11, {"tokens": fused_max})
+    assert e == "kern_mx_quant_routing" and p["grid"][0] == 1 + -(-fused_max * (K // 16) // 1024) == 256
+    for T in (fused_max + 1, 2048, 8192):
+        got = [e for e, _ in _runs(op, 11, {"tokens": T})]
+        want = [e for e, _ in _runs(mf.moe_routing(k, 0, 256), 8, {"tokens": T})] + ["kern_mx_quant_bf16"]
+        assert got == want, T
