@@ -280,6 +280,19 @@ def mxfp4_gemm_bf16(N: int, K: int, rows_var: str = "tokens") -> dict:
     return {"params": p, "impl": {"launches": [walk, {**tiled, "when": {"var": rows_var, "min": 65}}]}}
 
 
+def mxfp4_gemm_e4m3(N: int, K: int, rows_var: str = "tokens") -> dict:
+    """The dense MXFP4 x MXFP8 GEMM with per-tensor e4m3 out (C ABI kern_mxfp4_gemm_e4m3, config 3's prefill
+    GEMM): in u8 a [N][K/2], sf_a (repacked weights), b [M][K], sf_b (MXFP8 activations), out u8 c [M][N] =
+    e4m3(acc * d_scale[0]), in f32 d_scale [1]; M = the value of `rows_var`. One tiled launch, grid
+    [N/256, ceil(M/128)], with a null f32 debug pointer."""
+    assert N % 256 == 0 and K % 512 == 0
+    p = ["in buffer<u8>"] * 4 + ["out buffer<u8>", "in buffer<f32>"]
+    return {"params": p, "impl": {"launches": [{
+        "module": MODULE, "entry": "kern_mx_gemm_e4m3", "params": p + ["bytes<4>", "i32", "i32", "i64"],
+        "block": [BMM_THREADS, 1, 1], "grid": [N // 256, {"ceil_div": [rows_var, 128]}, 1],
+        "args": [{"param": i} for i in range(6)] + [_rows(rows_var), {"i32": N}, {"i32": K}, {"i64": 0}]}]}}
+
+
 QUANT_ROUTING_WORKGROUPS = 255  # quantizer workgroups the fused launch holds (one round beside the routing block)
 
 

@@ -235,3 +235,23 @@ def test_quant_routing_op_takes_the_c_abi_launches(ops, K, k, E, Ts):
             outs.append([q, qs] + tabs)
         for a, b in zip(*outs):
             assert torch.equal(a, b), T
+
+
+@pytest.mark.parametrize("N,K,M", [(2048, 7168, 4096), (512, 1024, 37)])
+def test_e4m3_gemm_op_matches_the_c_abi(ops, N, K, M):
+    """Config 3's prefill GEMM (per-tensor e4m3 out) as a manifest op, at its full shape and a ragged one."""
+    print(f"[manifest] mxfp4_gemm_e4m3 N={N} K={K} M={M}", flush=True)
+    op = ops.ManifestOp(mf.mxfp4_gemm_e4m3(N, K))
+    w, sf = wl.mxfp4_weights(350 + K, 1, N, K, 122, 132)
+    wp, sfp = ops.repack_weights(_dev(w[0]), _dev(sf[0]))
+    x = _dev(wl.activations_bf16(351, M, K))
+    q = torch.zeros((M, K), dtype=torch.uint8, device="cuda")
+    qs = torch.zeros((M, K // 32), dtype=torch.uint8, device="cuda")
+    ops.moe_quant(x, q, qs, M, K=K)
+    ds = torch.tensor([0.05], dtype=torch.float32, device="cuda")
+    c0 = torch.full((M, N), 0x5A, dtype=torch.uint8, device="cuda")
+    c1 = torch.full((M, N), 0x5A, dtype=torch.uint8, device="cuda")
+    ops.mxfp4_gemm_e4m3(wp, sfp, q, qs, c0, ds, M=M, m=N, k=K)
+    op(wp, sfp, q, qs, c1, ds, vars={"tokens": M})
+    torch.cuda.synchronize()
+    assert torch.equal(c0, c1)

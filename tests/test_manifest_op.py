@@ -276,6 +276,9 @@ def test_dense_gemm_op_plans(lib):
             assert p["grid"] == (9216 // 256, -(-M // 128), 1)
     (e, _), = _runs(mf.mxfp4_gemm_bf16(2048, 3584), 5, {"tokens": 8})  # K = 3584: no walk instance
     assert e == "kern_mx_gemm_bf16"
+    (e, p), = _runs(mf.mxfp4_gemm_e4m3(2048, 7168), 6, {"tokens": 4096})
+    assert e == "kern_mx_gemm_e4m3" and p["grid"] == (8, 32, 1) and struct.unpack_from("<iii", p["args"], 48) == \
+        (4096, 2048, 7168)
 
 
 def test_quant_routing_op_plans(lib):
