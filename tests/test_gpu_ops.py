@@ -530,7 +530,7 @@ def test_moe_finalize_bitexact(ops, oracle, T, H, k):
     np.testing.assert_array_equal(to_np(out).view(np.uint16), oracle.moe_finalize(fc2, e2p, w, None, T, H, k))
 
 
-@pytest.mark.parametrize("T,H,k", [(512, 7168, 8), (9, 3584, 16), (3, 8192, 2)])
+@pytest.mark.parametrize("T,H,k", [(512, 7168, 8), (9, 3584, 16), (3, 8192, 2), (5, 520, 4), (2, 8, 1)])
 def test_moe_finalize_rms(ops, oracle, T, H, k):
     rows = ((T * k + 127) // 128 + 4) * 128
     fc2, e2p, w = _finalize_case(T, H, k, rows, 50 + H)
