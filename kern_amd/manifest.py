@@ -235,8 +235,8 @@ def _gemv_launch(N: int, K: int, M: int, rows_var: str) -> dict:
 
 
 def _by_rows(launch_at, rows_var: str, lo: int, hi: int) -> list:
-    """Launches for rows lo..hi: launch_at(M) at each M, runs of equal launches merged into one `when` range
-    (a lower end of 1 and an upper end of `None` bound nothing)."""
+    """Launches for rows lo..hi: launch_at(M) at each M, each run of equal launches merged into one launch whose
+    `when` covers the run (min and max both given, so nothing runs outside lo..hi)."""
     out = []
     for M in range(lo, hi + 1):
         L = {"module": MODULE, **launch_at(M)}
