@@ -10,9 +10,9 @@ not change. Shape constants a launch needs (hidden size, expert count, top-k) ar
 as in the reference's own launches; `tokens` is the manifest var the grids read.
 
 The grammar is the reference's: grids are Expr trees (types.rs:1517-1576), args LaunchArg
-(types.rs:1174-1191). A launch arg cannot name a var directly, so the one kernel argument that is the
-var `tokens` (moe_routing's token count) travels as a 4-byte pack, the form the reference uses for
-struct-taking kernels (types.rs:1193-1260).
+(types.rs:1174-1191). A launch arg cannot name a var directly, so the kernel arguments that are the var
+`tokens` (moe_routing's token count, the dense ops' row count) travel as 4-byte packs, the form the
+reference uses for struct-taking kernels (types.rs:1193-1260).
 """
 from __future__ import annotations
 
@@ -118,8 +118,9 @@ def _slot_capacity(topk: int, experts: int) -> dict:
 
 def moe_fc1(m: int, k: int, experts: int, topk: int) -> dict:
     """moe_fc1 = trtllm_bmm_mxe4m3_mxe2m1_mxe4m3 (13 params); launch adds i32 m (= 2I), i32 k (= H), the slot
-    tables' capacity E + ceil(tokens*topk/128) and a null f32 debug pointer (an i64 zero). The kernel is persistent: grid [256, 1, 1], and each workgroup
-    loops over the live slots' tiles (num_non_exiting is read on the device), so the grid needs no var."""
+    tables' capacity E + ceil(tokens*topk/128) and a null f32 debug pointer (an i64 zero). The kernel is
+    persistent: grid [256, 1, 1], and each workgroup loops over the live slots' tiles (num_non_exiting is
+    read on the device), so the grid needs no var."""
     assert m % 256 == 0 and m <= 131072 and k % 512 == 0  # the kernels' tile lists hold m/256 < 512
     p = ["in buffer<u8>"] * 4 + ["out buffer<u8>"] * 2 + ["in buffer<i32>", "in buffer<f32>", "in buffer<f32>"] \
         + ["in buffer<i32>"] * 4
