@@ -341,6 +341,23 @@ def test_fc_ring_row_counts(ops, oracle):
     _check_fc2(ops, oracle, ids, 8, 512, 1024)
 
 
+def test_fc_most_experts(ops, oracle):
+    """512 local experts (the routing tables' maximum), about four rows each: every slot skinny."""
+    ids = wl.topk_ids(90, 256, 512, 8)
+    print("[fc max experts] E=512, T=256, top-8", flush=True)
+    _check_fc1(ops, oracle, ids, 512, 512, 1024)
+    _check_fc2(ops, oracle, ids, 512, 512, 1024)
+
+
+def test_fc_widest_weights(ops, oracle):
+    """m = 131072 weight rows (the largest the C ABI takes): 512 weight tiles per slot, so the walk's tile codes
+    reach nx = 511, on a skinny slot (4 rows) and a ring slot (20 rows)."""
+    ids = np.concatenate([np.zeros((4, 1), np.int32), np.ones((20, 1), np.int32)])
+    print("[fc widest] m=131072, K=512, slots of 4 and 20 rows", flush=True)
+    _check_fc1(ops, oracle, ids, 2, 131072, 512)
+    _check_fc2(ops, oracle, ids, 2, 131072, 512)
+
+
 def test_fc2_live_count_is_capped_by_the_tables(ops, oracle):
     """num_non_exiting larger than the slot tables (a corrupt count): the persistent kernel walks no slot past
     the tables' capacity; the live slots' rows come out as with the true count (the tables past the routed
