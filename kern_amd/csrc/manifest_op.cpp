@@ -299,6 +299,50 @@ struct kern_op_s {
 
 namespace {
 
+// The blocks kern_mx's entries are written for: their mapping of threads to work assumes these shapes (a
+// block of 256 lanes, the 8 waves of a GEMM workgroup with their roles, a 1024-lane routing workgroup), so a
+// launch with another block would compute something else without an error. Each needs block [x, 1, 1] with x
+// exactly the given count, or, where `per_wave`, any whole number of waves up to it. Entries of other modules
+// are not named here and are not checked.
+struct BlockRule {
+  const char* name;
+  bool prefix;  // the rule covers a family of instances (name followed by their suffix)
+  uint32_t x;
+  bool per_wave;
+};
+const BlockRule kBlockRules[] = {
+    {"kern_mx_quant_bf16", false, 256, false},      {"kern_mx_quant_f32", false, 256, false},
+    {"kern_mx_w_shuffle", false, 256, false},       {"kern_mx_sf_shuffle", false, 256, false},
+    {"kern_mx_gemv_bf16", false, 256, false},       {"kern_mx_gemv_bf16_rg", false, 256, false},
+    {"kern_mx_gemv_bf16_r", true, 256, false},      {"kern_mx_gemv_bf16_p", true, 512, false},
+    {"kern_mx_gemm_bf16_s", true, 512, false},      {"kern_mx_gemm_bf16", false, 512, false},
+    {"kern_mx_gemm_e4m3", false, 512, false},       {"kern_mx_gemm_mxfp8", false, 512, false},
+    {"kern_mx_bmm_fc1", false, 512, false},         {"kern_mx_bmm_fc2", false, 512, false},
+    {"kern_mx_routing", false, 1024, false},        {"kern_mx_routing_count", false, 1024, false},
+    {"kern_mx_routing_scan", false, 1024, false},   {"kern_mx_routing_rank", false, 1024, false},
+    {"kern_mx_quant_routing", false, 1024, false},  {"kern_silu_mul_bf16", false, 256, false},
+    {"kern_mx_moe_finalize", false, 256, false},    {"kern_mx_fill_random_u8", false, 256, false},
+    {"kern_mx_moe_finalize_rms", false, 1024, true},
+};
+
+// "" when the block suits the entry (or the entry has no rule), else the reason
+std::string block_rule_error(const std::string& entry, const uint32_t block[3]) {
+  const BlockRule* hit = nullptr;
+  for (const BlockRule& r : kBlockRules) {
+    const size_t n = strlen(r.name);
+    const bool match = r.prefix ? entry.size() > n && entry.compare(0, n, r.name) == 0 && entry != "kern_mx_gemv_bf16_rg"
+                                : entry == r.name;
+    if (match) hit = &r;
+  }
+  if (!hit) return "";
+  const uint32_t x = block[0];
+  const bool ok = block[1] == 1 && block[2] == 1 && (hit->per_wave ? x % 64 == 0 && x <= hit->x : x == hit->x);
+  if (ok) return "";
+  return "`" + entry + "` is written for block " +
+         (hit->per_wave ? "[64·n, 1, 1] with 64·n <= " + std::to_string(hit->x) : "[" + std::to_string(hit->x) + ", 1, 1]") +
+         ", not [" + std::to_string(block[0]) + ", " + std::to_string(block[1]) + ", " + std::to_string(block[2]) + "]";
+}
+
 bool parse_op(const char* json, kern_op_s& op, std::string& err) {
   JVal root;
   if (!parse_json(json, root, err)) return err = "op JSON: " + err, false;
@@ -362,6 +406,7 @@ bool parse_op(const char* json, kern_op_s& op, std::string& err) {
       threads *= l.block[i];
     }
     if (threads > 1024) return err = ctx + ": block exceeds 1024 threads (gfx950)", false;
+    if (const std::string why = block_rule_error(l.entry, l.block); !why.empty()) return err = ctx + ": " + why, false;
     const JVal* g = L.get("grid");
     if (!g || g->kind != JVal::Arr || g->a.size() != 3) return err = ctx + ": `grid` must be [x, y, z]", false;
     for (int i = 0; i < 3; ++i)

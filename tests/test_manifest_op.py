@@ -293,3 +293,27 @@ def test_quant_routing_op_plans(lib):
         got = [e for e, _ in _runs(op, 11, {"tokens": T})]
         want = [e for e, _ in _runs(mf.moe_routing(k, 0, 256), 8, {"tokens": T})] + ["kern_mx_quant_bf16"]
         assert got == want, T
+
+
+@pytest.mark.parametrize("op,block,ok", [
+    (mf.moe_fc2(1024, 512, 8, 2), [256, 1, 1], False),       # the GEMM's eight waves have roles
+    (mf.moe_fc2(1024, 512, 8, 2), [512, 2, 1], False),
+    (mf.moe_routing(8, 0, 64), [512, 1, 1], False),
+    (mf.moe_quant(1024), [128, 1, 1], False),                 # lanes index 256-lane blocks
+    (mf.mxfp4_gemv_bf16(512, 1024), [512, 1, 1], False),      # kern_mx_gemv_bf16_r2
+    (mf.moe_finalize_rms(7168, 8), [100, 1, 1], False),       # whole waves only
+    (mf.moe_finalize_rms(7168, 8), [256, 1, 1], True),        # fewer threads than chunks: still correct
+    (mf.moe_finalize_rms(7168, 8), [1024, 1, 1], True),
+])
+def test_blocks_the_entries_are_written_for(lib, op, block, ok):
+    """A launch of a kern_mx entry with a block its thread mapping was not written for is refused when the op
+    is read (here through the host-only plan), naming the block it needs."""
+    import copy
+    op = copy.deepcopy(op)
+    op["impl"]["launches"][0]["block"] = block
+    n = len(op["params"])
+    if ok:
+        ops.op_plan(op, 0, [0x1000] * n, {"tokens": 4})
+    else:
+        with pytest.raises(ops.KernError, match="is written for block"):
+            ops.op_plan(op, 0, [0x1000] * n, {"tokens": 4})
