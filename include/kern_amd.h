@@ -108,7 +108,8 @@ typedef struct kern_op_s* kern_op;
  * the manifest's `modules` table names `module_name`, and check its params against the code object's
  * kernel-argument sizes (compile.rs:385-415). Extern launches, scratch buffers, rank args, TMA
  * descriptors, clusters and programmatic dependent launch have no gfx950 counterpart here:
- * KERN_ERR_MANIFEST. */
+ * KERN_ERR_MANIFEST. So is a launch of one of kern_mx's entries with a block other than the one its mapping
+ * of threads to work is written for (the message names it; kern_op_plan and kern_op_verify refuse it too). */
 int kern_op_create(const char* op_json, const char* module_name, kern_module mod, kern_op* out);
 int kern_op_destroy(kern_op op);
 int kern_op_num_params(kern_op op);   /* -1 for a null op */
