@@ -1748,8 +1748,13 @@ KERN_DEV void bmm_moe(const BmmArgs& A, const BmmLds& L, int* list, int* lexp, i
 #ifdef KERN_CLOCK_PROBE
 #define CLOCK_PROBE_BEGIN()                                                  \
   const uint64_t ck_t0 = __builtin_amdgcn_s_memtime(), ck_r0 = __builtin_amdgcn_s_memrealtime()
+// The end stamps follow a barrier, so they mark the workgroup's last wave, not wave 0's. Where waves run
+// apart (the persistent MoE kernels' small-tile quarters), the older of the two waves that share a SIMD
+// issues first and can end up to 200 us before the other: FC1 at T = 64 measured wave 0's span at 326 us,
+// the last waves' at 506 us, and the launch at 514 us.
 #define CLOCK_PROBE_END(buf)                                                                          \
   do {                                                                                                \
+    __syncthreads();                                                                                  \
     const uint64_t ck_t1 = __builtin_amdgcn_s_memtime(), ck_r1 = __builtin_amdgcn_s_memrealtime();    \
     if ((buf) && threadIdx.x == 0) {                                                                  \
       uint64_t* o = reinterpret_cast<uint64_t*>(buf) + 4 * (blockIdx.x + gridDim.x * blockIdx.y);     \
