@@ -831,18 +831,10 @@ struct BmmArgs {
 // The LDS address of a generic pointer into LDS is its low 32 bits (the shared aperture sits in the high
 // half): taken that way, with no address-space cast, and so no null check on each request.
 KERN_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
-KERN_DEV void dma16(const void* g, void* lds_wave_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-// 4 bytes per lane, to `lds_wave_base + 4 * lane`
-KERN_DEV void dma4(const void* g, void* lds_wave_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-// The same requests with a wave-uniform base in an SGPR pair and a per-lane 32-bit byte offset (the
-// instructions' SADDR form): the per-lane address needs no 64-bit add per request, and a k step moves the
-// base once for all of a wave's requests into that buffer.
+// The requests take a wave-uniform base in an SGPR pair and a per-lane 32-bit byte offset (the instructions'
+// SADDR form): the per-lane address needs no 64-bit add per request, and a k step moves the base once for all
+// of a wave's requests into that buffer. dma16s moves 16 bytes per lane, dma4s 4 bytes per lane (to
+// `lds_wave_base + 4 * lane`).
 KERN_DEV uint64_t uniform_ptr(const void* p) {
   const uint64_t b = (uint64_t)(uintptr_t)p;
   // readfirstlane returns an int: each half goes through uint32_t, so the low half is not sign-extended

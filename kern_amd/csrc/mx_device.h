@@ -46,46 +46,6 @@ KERN_DEV uint32_t bf16x2_hw(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2bf));
 }
 
-// RNE of mant >> s for s in [1, 31]
-KERN_DEV uint32_t rne_shr(uint32_t mant, uint32_t s) {
-  uint32_t q = mant >> s;
-  uint32_t rem = mant & ((1u << s) - 1u);
-  uint32_t half = 1u << (s - 1u);
-  return q + ((rem > half) | ((rem == half) & (q & 1u)));
-}
-
-// e4m3fn code of (f32 with bits `bits`) * 2^shift, round-to-nearest-even, saturating.
-KERN_DEV uint32_t e4m3_rne(uint32_t bits, int shift) {
-  uint32_t sign = (bits >> 24) & 0x80u;
-  uint32_t a = bits & 0x7fffffffu;
-  if (a >= 0x7f800000u) return sign | (a == 0x7f800000u ? 0x7eu : 0x7fu);
-  if (a == 0) return sign;
-  int E = (int)(a >> 23);
-  uint32_t mant;
-  int e;
-  if (E != 0) {
-    mant = (a & 0x7fffffu) | 0x800000u;
-    e = E - 127;
-  } else {  // f32 subnormal: normalise so bit 23 is set
-    uint32_t m = a & 0x7fffffu;
-    int lz = __clz(m) - 8;
-    mant = m << lz;
-    e = -126 - lz;
-  }
-  e += shift;
-  if (e >= -6) {
-    uint32_t r = rne_shr(mant, 20);  // 8..16
-    int ef = e + 7 + (int)(r >> 4);
-    uint32_t code = ((uint32_t)ef << 3) | (r & 7u);
-    if (ef > 15) code = 0x7eu;
-    code = code > 0x7eu ? 0x7eu : code;
-    return sign | code;
-  }
-  int s = 14 - e;  // >= 21
-  uint32_t q = s >= 32 ? 0u : rne_shr(mant, (uint32_t)s);
-  return sign | q;
-}
-
 // MXFP8 scale code for a block whose largest |bits| is amax: floor(log2 amax) - 8 + 127 clamped to [0, 254] for
 // a finite amax, 255 for a non-finite one (amax_bits >= 0x7f800000). A normal amax has floor(log2) = E - 127 for
 // its exponent field E <= 254, so the code is E - 8; a subnormal or zero amax (E = 0) gives a negative code,
@@ -95,22 +55,9 @@ KERN_DEV uint32_t mx_scale_code(uint32_t amax_bits) {
   return E >= 255u ? 255u : (E > 8u ? E - 8u : 0u);
 }
 
-// element code of an f32 value in a block with scale code `sc`
-KERN_DEV uint32_t mx_elem_code(uint32_t bits, uint32_t sc) {
-  if (sc == 255u) return ((bits >> 24) & 0x80u) | 0x7fu;
-  return e4m3_rne(bits, 127 - (int)sc);
-}
-
-// e4m3fn code of f32 `f` through the hardware converter: RNE, saturating to +-448 by clamping first,
-// NaN -> 0x7f|sign. Bit-identical to e4m3_rne(bits, 0) for every input (checked on gfx950 over all
-// bf16 values at shifts -20..126).
-KERN_DEV uint32_t e4m3_hw(float f) {
-  if (__builtin_isnan(f)) return ((__float_as_uint(f) >> 24) & 0x80u) | 0x7fu;
-  const float c = __builtin_fminf(__builtin_fmaxf(f, -448.0f), 448.0f);
-  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, c, 0, false) & 0xffu;
-}
-
-// two e4m3 codes (low byte = a) of finite-or-not f32 values, RNE saturating
+// two e4m3fn codes (low byte = a) of f32 values through the hardware converter: RNE, saturating to +-448
+// by clamping first, NaN -> 0x7f|sign. Each code is bit-identical to an integer round-to-nearest-even
+// encoder of the value (the CPU oracle's), checked on gfx950 over all bf16 values at shifts -20..126.
 KERN_DEV uint32_t e4m3_hw2(float a, float b) {
   const float ca = __builtin_fminf(__builtin_fmaxf(a, -448.0f), 448.0f);
   const float cb = __builtin_fminf(__builtin_fmaxf(b, -448.0f), 448.0f);
