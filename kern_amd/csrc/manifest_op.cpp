@@ -747,7 +747,7 @@ extern "C" int kern_op_launch(kern_op op, const uint64_t* params, int nparams, c
     if (!plan_launch(*op, l, params, vars, pl, err))
       return kern_amd_fail(KERN_ERR_CALL, "op launch #%zu (%s): %s", li, l.entry.c_str(), err.c_str());
     if (pl.skip) continue;
-    if (int rc = kern_launch(l.fn, pl.grid, l.block, pl.shared, stream, pl.args.data(), pl.args.size()))
+    if (kern_launch(l.fn, pl.grid, l.block, pl.shared, stream, pl.args.data(), pl.args.size()) != KERN_OK)
       return kern_amd_fail(KERN_ERR_CALL, "op launch #%zu (%s): %s", li, l.entry.c_str(), kern_last_error());
   }
   return KERN_OK;
